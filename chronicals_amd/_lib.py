@@ -1,0 +1,109 @@
+"""ctypes binding of libchronicals_cce.so (declared in include/chronicals_cce.h).
+
+Loading fails loudly: there is no CPU or PyTorch fallback for this path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+from . import build as _build
+
+# constants mirrored from include/chronicals_cce.h
+CCE_ABI_VERSION = 1
+CCE_OK = 0
+CCE_ERR_INVALID_ARG = 1
+CCE_ERR_WORKSPACE = 2
+CCE_ERR_HIP = 3
+CCE_REDUCTION_NONE = 0
+CCE_REDUCTION_MEAN = 1
+CCE_REDUCTION_SUM = 2
+CCE_DTYPE_BF16 = 0
+CCE_DTYPE_F32 = 1
+
+REDUCTIONS = {"none": CCE_REDUCTION_NONE, "mean": CCE_REDUCTION_MEAN, "sum": CCE_REDUCTION_SUM}
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "cce_abi_version": (_i32, []),
+    "cce_last_error": (ctypes.c_char_p, []),
+    "cce_forward_workspace_bytes": (_i32, [_i64, _i64, _i64, _i32, ctypes.POINTER(_sz)]),
+    "cce_backward_workspace_bytes": (_i32, [_i64, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_sz)]),
+    "cce_forward": (_i32, [
+        _vp, _vp, _vp, _i32, _vp,            # hidden, weight, labels, labels_int64, bias
+        _i64, _i64, _i64, _i64,              # N, d, V, ignore_index
+        _f32, _f32, _i32,                    # label_smoothing, z_loss_weight, reduction
+        _vp, _vp, _vp,                       # loss_out, lse_out, n_valid_out
+        _vp, _sz, _vp,                       # workspace, workspace_bytes, stream
+    ]),
+    "cce_backward": (_i32, [
+        _vp, _vp, _vp, _vp, _i32, _vp,       # grad_out, hidden, weight, labels, labels_int64, bias
+        _vp, _vp,                            # lse, n_valid
+        _i64, _i64, _i64, _i64,              # N, d, V, ignore_index
+        _f32, _f32, _i32, _i64,              # label_smoothing, z_loss_weight, reduction, chunk_size
+        _vp, _i32, _vp, _i32, _vp,           # grad_hidden, dtype, grad_weight, dtype, grad_bias
+        _vp, _sz, _vp,                       # workspace, workspace_bytes, stream
+    ]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class CCEError(RuntimeError):
+    """A non-zero return from libchronicals_cce."""
+
+
+def lib_path() -> str:
+    return os.environ.get("CHRONICALS_CCE_LIB", _build.LIB_PATH)
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = lib_path()
+        if not os.path.exists(path):
+            raise ImportError(
+                f"libchronicals_cce.so not found at {path}: build it with "
+                f"`python -m chronicals_amd.build` (or __graft_entry__.build())"
+            )
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        ver = lib.cce_abi_version()
+        if ver != CCE_ABI_VERSION:
+            raise ImportError(f"libchronicals_cce ABI version {ver}, expected {CCE_ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def check(rc: int) -> None:
+    if rc != CCE_OK:
+        msg = load().cce_last_error()
+        raise CCEError(f"libchronicals_cce error {rc}: {msg.decode() if msg else ''}")
+
+
+def forward_workspace_bytes(N: int, d: int, V: int, reduction: int) -> int:
+    out = _sz(0)
+    check(load().cce_forward_workspace_bytes(N, d, V, reduction, ctypes.byref(out)))
+    return out.value
+
+
+def backward_workspace_bytes(N: int, d: int, V: int, chunk_size: int, need_dh: bool, need_dw: bool) -> int:
+    out = _sz(0)
+    check(load().cce_backward_workspace_bytes(N, d, V, chunk_size, int(need_dh), int(need_dw), ctypes.byref(out)))
+    return out.value

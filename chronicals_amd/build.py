@@ -1,0 +1,62 @@
+"""Build libchronicals_cce.so (HIP, gfx950) in-tree with hipcc.
+
+The library is compiled from ``chronicals_amd/csrc/cce_kernels.hip`` into
+``chronicals_amd/lib/libchronicals_cce.so``; the package loads it from there
+with ctypes.  Building always recompiles.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+SRC = os.path.join(PKG_DIR, "csrc", "cce_kernels.hip")
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+LIB_NAME = "libchronicals_cce.so"
+LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
+ARCH = "gfx950"
+
+
+def hipcc_path() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found: the HIP toolchain (ROCm) is required to build chronicals_amd")
+
+
+def compile_command(out_path: str) -> list:
+    return [
+        hipcc_path(),
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        # packed fp32 VALU ops stay off (the compiler may not form them)
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-I", os.path.join(REPO_DIR, "include"),
+        "-o", out_path,
+        SRC,
+    ]
+
+
+def build(verbose: bool = False) -> str:
+    """Compile the HIP library; returns the path of the built .so."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = LIB_PATH + f".tmp{os.getpid()}"
+    cmd = compile_command(tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,1043 @@
+// Fused linear cross-entropy (Cut Cross-Entropy) for MI355X / gfx950.
+//
+// The lm_head projection S = H . W^T (H [N,d] bf16, W [V,d] bf16) and the
+// softmax cross-entropy over the vocabulary are computed without ever writing
+// the N x V logits to HBM:
+//
+//   forward   one bf16 MFMA GEMM over (256-row tile) x (run of 256-column
+//             vocabulary tiles) whose epilogue keeps a per-row online
+//             (max, sum-exp) in registers; a per-row combine kernel merges the
+//             vocabulary splits, gathers the target logit and forms the loss.
+//   backward  per vocabulary band (chunk_size columns): a recompute GEMM
+//             whose epilogue forms G = dLoss/dS in bf16 for the band
+//             (softmax - one-hot, masking, scaling), then two MFMA GEMMs
+//             dH += G . W_band and dW_band = G^T . H.  Only the band of G
+//             (N x chunk) exists in memory; its size is bounded by chunk_size.
+//
+// Semantics follow chronicals/kernels/cut_cross_entropy.py (reference):
+//   forward   :567-692  lse = m + log(s + 1e-10); ce = lse - t;
+//                        (1-eps)*ce + eps*log(V); + z*lse^2; masked mean
+//   backward  :703-808  G = P - (1-eps)*onehot - eps/V + 2z*lse*P,
+//                        times valid * grad_out / n_valid; dH = G W; dW = G^T H
+// with the one-hot term applied (the reference's CPU path drops it at
+// :773-780; its GPU path :530-546 and triton_kernels.py:2594-2601 apply it).
+//
+// All device work is launched on the caller's stream; there are no host
+// synchronisations and no device allocations: scratch memory is a caller
+// workspace whose size the *_workspace_bytes entry points report.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <math.h>
+#include <float.h>
+
+#include "../../include/chronicals_cce.h"
+
+namespace {
+
+typedef uint16_t bf16_t;  // raw bf16 storage
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 512;         // 8 waves of 64
+constexpr int kBM = 256;              // rows of a workgroup tile
+constexpr int kBK = 64;               // K slab per pipeline step
+constexpr int kPitch = kBK + 8;       // LDS row pitch in bf16 (144 B: conflict-free b128 reads)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.69314718055994531f;
+constexpr float kNegBig = -FLT_MAX;   // finite "minus infinity" for running maxima
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ inline f32x4 mfma_16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+  const __bf16 a = (__bf16)lo, b = (__bf16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+__device__ inline float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// ---------------------------------------------------------------------------
+// Workgroup -> tile mapping.  The hardware deals consecutive workgroup ids to
+// the 8 XCDs round-robin; remap so that each XCD receives a contiguous range
+// of logical tiles, then walk logical tiles in groups of 4 row tiles so the
+// ~32 workgroups resident on one XCD share 4 row tiles of A and 8 column
+// tiles of B through that XCD's L2.
+// ---------------------------------------------------------------------------
+__device__ inline void grouped_map(int bid, int nb, int gm, int gn, int& pm, int& pn) {
+  const int per = nb >> 3;
+  const int u = (bid < per * 8) ? ((bid & 7) * per + (bid >> 3)) : bid;
+  constexpr int G = 4;
+  const int width = G * gn;
+  const int grp = u / width;
+  const int first = grp * G;
+  const int rows = min(gm - first, G);
+  const int r = u - grp * width;
+  pm = first + r % rows;
+  pn = r / rows;
+}
+
+// ---------------------------------------------------------------------------
+// Global -> LDS operand loaders.  LDS holds every operand tile as [row][k]
+// (k contiguous, pitch kPitch) so one MFMA fragment read serves both layouts.
+// ---------------------------------------------------------------------------
+
+// K-major operand: element (r, k) at X[r*ld + k].
+template <int BR>
+struct LoadKMajor {
+  static constexpr int kN = BR * (kBK / 8) / kThreads;  // 16-byte chunks per thread
+  u32x4 v[kN];
+  __device__ inline void load(const bf16_t* __restrict__ X, long ld, int r0, int rlim, int k0, int K,
+                              int tid) {
+#pragma unroll
+    for (int i = 0; i < kN; ++i) {
+      const int c = tid + i * kThreads;
+      const int row = c >> 3, kc = (c & 7) * 8;
+      const int gr = r0 + row, gk = k0 + kc;
+      if (gr < rlim && gk < K)
+        v[i] = *reinterpret_cast<const u32x4*>(X + (long)gr * ld + gk);
+      else
+        v[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  __device__ inline void store(bf16_t* S, int tid) const {
+#pragma unroll
+    for (int i = 0; i < kN; ++i) {
+      const int c = tid + i * kThreads;
+      const int row = c >> 3, kc = (c & 7) * 8;
+      *reinterpret_cast<u32x4*>(S + row * kPitch + kc) = v[i];
+    }
+  }
+};
+
+// MN-major operand (256-row tiles): element (r, k) at X[k*ld + r].  Each
+// thread loads a 4(k) x 8(r) block with four 16-byte loads, transposes it in
+// registers and writes eight 8-byte [r][k] pieces to LDS.  Lanes 0..15 of a
+// wave walk k, so the 8-byte LDS writes of 16 lanes cover 32 distinct banks.
+struct LoadMNMajor256 {
+  u32x4 v[4];
+  __device__ inline void load(const bf16_t* __restrict__ X, long ld, int r0, int rlim, int k0, int K,
+                              int tid) {
+    const int w = tid >> 6, l = tid & 63;
+    const int kq = l & 15, rb = (w << 2) + (l >> 4);
+    const int gr = r0 + rb * 8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int gk = k0 + kq * 4 + i;
+      if (gk < K && gr < rlim)
+        v[i] = *reinterpret_cast<const u32x4*>(X + (long)gk * ld + gr);
+      else
+        v[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  __device__ inline void store(bf16_t* S, int tid) const {
+    const int w = tid >> 6, l = tid & 63;
+    const int kq = l & 15, rb = (w << 2) + (l >> 4);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t a0 = v[0][q], a1 = v[1][q], a2 = v[2][q], a3 = v[3][q];
+      const u32x2 ev = {(a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16)};
+      const u32x2 od = {(a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u)};
+      *reinterpret_cast<u32x2*>(S + (rb * 8 + 2 * q) * kPitch + kq * 4) = ev;
+      *reinterpret_cast<u32x2*>(S + (rb * 8 + 2 * q + 1) * kPitch + kq * 4) = od;
+    }
+  }
+};
+
+template <bool KMAJ, int BR>
+struct LoaderSel {
+  typedef LoadKMajor<BR> type;
+};
+template <>
+struct LoaderSel<false, 256> {
+  typedef LoadMNMajor256 type;
+};
+
+struct GemmShape {
+  const bf16_t* A;  // M x K operand
+  long lda;
+  const bf16_t* B;  // N x K operand
+  long ldb;
+  int M, N, K;
+};
+
+// One BK=64 slab of MFMA work for a wave: wave tile 64 x (BN/2), 16x16x32
+// instructions.  The B fragment is passed as the instruction's first operand,
+// so the accumulator holds C^T in the hardware's 16x16 layout: lane l owns
+// C[m = i*16 + (l & 15)][n = j*16 + (l >> 4)*4 + r], r = 0..3 (four
+// consecutive columns of one row).
+template <int BN>
+__device__ inline void mma_slab(const bf16_t* __restrict__ As, const bf16_t* __restrict__ Bs,
+                                f32x4 (&acc)[4][BN / 32], int wm, int wn, int l) {
+  constexpr int FN = BN / 32;
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const int kof = kk * 32 + (l >> 4) * 8;
+    u32x4 a[4], b[FN];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      a[i] = *reinterpret_cast<const u32x4*>(As + (wm * 64 + i * 16 + (l & 15)) * kPitch + kof);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      b[j] = *reinterpret_cast<const u32x4*>(Bs + (wn * (BN / 2) + j * 16 + (l & 15)) * kPitch + kof);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = mfma_16x16x32(b[j], a[i], acc[i][j]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Epilogues
+// ---------------------------------------------------------------------------
+
+// Forward: per-row online (max, sum-exp) in base 2 over the workgroup's run of
+// vocabulary tiles; at the end one partial per (row, split) is written.
+template <int BN>
+struct EpiLse {
+  struct Params {
+    const float* bias;  // [V] or null
+    float* pm;          // [splits][M] running max (log2 units)
+    float* ps;          // [splits][M] sum of 2^(x - max)
+    int splits;
+    int tiles_n;
+  };
+  struct State {
+    float m[4], s[4];
+  };
+  static __device__ inline void assign(const GemmShape& g, const Params& p, int bid, int nb, int& tm,
+                                       int& t0, int& t1, int& split) {
+    const int gm = (g.M + kBM - 1) / kBM;
+    int s;
+    grouped_map(bid, nb, gm, p.splits, tm, s);
+    split = s;
+    t0 = (int)(((long)p.tiles_n * s) / p.splits);
+    t1 = (int)(((long)p.tiles_n * (s + 1)) / p.splits);
+  }
+  static __device__ inline void init(State& st) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      st.m[i] = kNegBig;
+      st.s[i] = 0.f;
+    }
+  }
+  static __device__ inline void tile(const Params& p, State& st, f32x4 (&acc)[4][BN / 32],
+                                     const GemmShape& g, int tm, int tn, int wm, int wn, int l) {
+    constexpr int FN = BN / 32;
+    float add[FN * 4];
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int col = tn * BN + wn * (BN / 2) + j * 16 + (l >> 4) * 4 + r;
+        add[j * 4 + r] = (col < g.N) ? (p.bias ? p.bias[col] : 0.f) : -INFINITY;
+      }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float x[FN * 4];
+      float mx = kNegBig;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v = (acc[i][j][r] + add[j * 4 + r]) * kLog2e;
+          x[j * 4 + r] = v;
+          mx = fmaxf(mx, v);
+        }
+      const float mn = fmaxf(st.m[i], mx);
+      float sum = 0.f;
+#pragma unroll
+      for (int q = 0; q < FN * 4; ++q) sum += fast_exp2(x[q] - mn);
+      st.s[i] = st.s[i] * fast_exp2(st.m[i] - mn) + sum;
+      st.m[i] = mn;
+    }
+  }
+  static __device__ inline void merge(float& m, float& s, float m2, float s2) {
+    const float mn = fmaxf(m, m2);
+    s = s * fast_exp2(m - mn) + s2 * fast_exp2(m2 - mn);
+    m = mn;
+  }
+  static __device__ inline void finish(const Params& p, State& st, const GemmShape& g, int tm, int split,
+                                       bf16_t* smem, int wm, int wn, int l) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      merge(st.m[i], st.s[i], __shfl_xor(st.m[i], 16), __shfl_xor(st.s[i], 16));
+      merge(st.m[i], st.s[i], __shfl_xor(st.m[i], 32), __shfl_xor(st.s[i], 32));
+    }
+    float* red = reinterpret_cast<float*>(smem);
+    if (wn == 1 && l < 16) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = wm * 64 + i * 16 + l;
+        red[row] = st.m[i];
+        red[kBM + row] = st.s[i];
+      }
+    }
+    __syncthreads();
+    if (wn == 0 && l < 16) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = wm * 64 + i * 16 + l;
+        merge(st.m[i], st.s[i], red[row], red[kBM + row]);
+        const int grow = tm * kBM + row;
+        if (grow < g.M) {
+          p.pm[(long)split * g.M + grow] = st.m[i];
+          p.ps[(long)split * g.M + grow] = st.s[i];
+        }
+      }
+    }
+  }
+};
+
+// Backward recompute: G[n][c] = dLoss/dS for one vocabulary band, stored bf16.
+// rowp[n] = {lse*log2e, cP, cT, cU}: g = cP*2^(x*log2e - lse2) - cU - cT*[c == label].
+template <int BN>
+struct EpiGrad {
+  struct Params {
+    const float* bias;     // [V] or null (full vocabulary, indexed by v0 + c)
+    const float4* rowp;    // [M]
+    const int* rowlab;     // [M] target column or -1
+    bf16_t* G;             // [M][ldg]
+    long ldg;
+    int v0;                // first vocabulary row of the band
+  };
+  struct State {};
+  static __device__ inline void assign(const GemmShape& g, const Params&, int bid, int nb, int& tm, int& t0,
+                                       int& t1, int& split) {
+    const int gm = (g.M + kBM - 1) / kBM, gn = (g.N + BN - 1) / BN;
+    int tn;
+    grouped_map(bid, nb, gm, gn, tm, tn);
+    t0 = tn;
+    t1 = tn + 1;
+    split = 0;
+  }
+  static __device__ inline void init(State&) {}
+  static __device__ inline void tile(const Params& p, State&, f32x4 (&acc)[4][BN / 32], const GemmShape& g,
+                                     int tm, int tn, int wm, int wn, int l) {
+    constexpr int FN = BN / 32;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = tm * kBM + wm * 64 + i * 16 + (l & 15);
+      if (m >= g.M) continue;
+      const float4 rp = p.rowp[m];
+      const int lab = p.rowlab[m] - p.v0;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int cb = tn * BN + wn * (BN / 2) + j * 16 + (l >> 4) * 4;
+        float gv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int col = cb + r;
+          float gg = 0.f;
+          if (col < g.N) {
+            const float b = p.bias ? p.bias[p.v0 + col] : 0.f;
+            const float x = (acc[i][j][r] + b) * kLog2e - rp.x;
+            gg = rp.y * fast_exp2(x) - rp.w;
+            if (col == lab) gg -= rp.z;
+          }
+          gv[r] = gg;
+        }
+        const u32x2 pk = {pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3])};
+        *reinterpret_cast<u32x2*>(p.G + (long)m * p.ldg + cb) = pk;
+      }
+    }
+  }
+  static __device__ inline void finish(const Params&, State&, const GemmShape&, int, int, bf16_t*, int, int,
+                                       int) {}
+};
+
+// Plain GEMM output with optional fp32 accumulation buffer.
+//   mode 0: out = C            1: acc32 = C
+//   mode 2: acc32 += C          3: out = acc32 + C
+template <int BN>
+struct EpiAcc {
+  struct Params {
+    float* acc32;
+    long ldacc;
+    void* out;
+    long ldo;
+    int out_f32;  // 0: bf16 output, 1: fp32 output
+    int mode;
+  };
+  struct State {};
+  static __device__ inline void assign(const GemmShape& g, const Params&, int bid, int nb, int& tm, int& t0,
+                                       int& t1, int& split) {
+    const int gm = (g.M + kBM - 1) / kBM, gn = (g.N + BN - 1) / BN;
+    int tn;
+    grouped_map(bid, nb, gm, gn, tm, tn);
+    t0 = tn;
+    t1 = tn + 1;
+    split = 0;
+  }
+  static __device__ inline void init(State&) {}
+  static __device__ inline void tile(const Params& p, State&, f32x4 (&acc)[4][BN / 32], const GemmShape& g,
+                                     int tm, int tn, int wm, int wn, int l) {
+    constexpr int FN = BN / 32;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = tm * kBM + wm * 64 + i * 16 + (l & 15);
+      if (m >= g.M) continue;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = tn * BN + wn * (BN / 2) + j * 16 + (l >> 4) * 4;
+        if (n >= g.N) continue;
+        f32x4 v = acc[i][j];
+        if (p.mode >= 2) v += *reinterpret_cast<const f32x4*>(p.acc32 + (long)m * p.ldacc + n);
+        if (p.mode == 1 || p.mode == 2) {
+          *reinterpret_cast<f32x4*>(p.acc32 + (long)m * p.ldacc + n) = v;
+        } else if (p.out_f32) {
+          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + (long)m * p.ldo + n) = v;
+        } else {
+          const u32x2 pk = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+          *reinterpret_cast<u32x2*>(reinterpret_cast<bf16_t*>(p.out) + (long)m * p.ldo + n) = pk;
+        }
+      }
+    }
+  }
+  static __device__ inline void finish(const Params&, State&, const GemmShape&, int, int, bf16_t*, int, int,
+                                       int) {}
+};
+
+// ---------------------------------------------------------------------------
+// The GEMM kernel: C[M,N] = A[M,K] . B[N,K]^T with a 2-stage LDS pipeline
+// (register-staged prefetch of slab s+1 while slab s feeds the MFMAs; one
+// barrier per slab).  A workgroup may own a run of column tiles (forward),
+// which the pipeline walks without draining between tiles.
+// ---------------------------------------------------------------------------
+template <int BN, bool AK, bool BK, template <int> class EpiT>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmShape g, typename EpiT<BN>::Params ep) {
+  typedef EpiT<BN> Epi;
+  constexpr int FN = BN / 32;
+  constexpr int kStage = (kBM + BN) * kPitch;
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * kStage];
+
+  const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
+  const int wm = w >> 1, wn = w & 1;
+
+  int tm, t0, t1, split;
+  Epi::assign(g, ep, blockIdx.x, gridDim.x, tm, t0, t1, split);
+  if (t0 >= t1) return;  // uniform for the whole workgroup
+
+  typename LoaderSel<AK, kBM>::type la;
+  typename LoaderSel<BK, BN>::type lb;
+  typename Epi::State st;
+  Epi::init(st);
+
+  f32x4 acc[4][FN];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = (g.K + kBK - 1) / kBK;
+  const int nsteps = (t1 - t0) * KT;
+  const int a_r0 = tm * kBM;
+
+  // prologue: slab 0 of tile t0
+  la.load(g.A, g.lda, a_r0, g.M, 0, g.K, tid);
+  lb.load(g.B, g.ldb, t0 * BN, g.N, 0, g.K, tid);
+  la.store(smem, tid);
+  lb.store(smem + kBM * kPitch, tid);
+  __syncthreads();
+
+  int kt = 0, tn = t0;          // slab/tile being computed
+  int nkt = 1, ntn = t0;        // slab/tile being prefetched
+  if (nkt == KT) { nkt = 0; ++ntn; }
+  for (int s = 0; s < nsteps; ++s) {
+    const int cur = s & 1;
+    const bool more = (s + 1 < nsteps);
+    if (more) {
+      la.load(g.A, g.lda, a_r0, g.M, nkt * kBK, g.K, tid);
+      lb.load(g.B, g.ldb, ntn * BN, g.N, nkt * kBK, g.K, tid);
+    }
+    mma_slab<BN>(smem + cur * kStage, smem + cur * kStage + kBM * kPitch, acc, wm, wn, l);
+    if (more) {
+      la.store(smem + (cur ^ 1) * kStage, tid);
+      lb.store(smem + (cur ^ 1) * kStage + kBM * kPitch, tid);
+      if (++nkt == KT) { nkt = 0; ++ntn; }
+    }
+    __syncthreads();
+    if (++kt == KT) {
+      Epi::tile(ep, st, acc, g, tm, tn, wm, wn, l);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      kt = 0;
+      ++tn;
+    }
+  }
+  Epi::finish(ep, st, g, tm, split, smem, wm, wn, l);
+}
+
+// ---------------------------------------------------------------------------
+// Auxiliary kernels
+// ---------------------------------------------------------------------------
+
+__device__ inline long load_label(const void* labels, int is64, long n) {
+  return is64 ? reinterpret_cast<const int64_t*>(labels)[n] : (long)reinterpret_cast<const int32_t*>(labels)[n];
+}
+
+// One wave per row: merge the vocabulary-split partials into lse, gather the
+// target logit (fp32 dot product of H[n] and W[label]) and form the per-row
+// loss.  Each block (4 rows) writes one partial (loss sum, valid count).
+__global__ __launch_bounds__(256) void fwd_combine_kernel(
+    const float* __restrict__ pm, const float* __restrict__ ps, int splits, const bf16_t* __restrict__ H,
+    const bf16_t* __restrict__ W, const void* labels, int labels64, const float* __restrict__ bias, int N, int d,
+    int V, long ignore_index, float eps, float zw, float logV, float* __restrict__ lse_out,
+    float* __restrict__ rowloss, float* __restrict__ bsum, int* __restrict__ bcnt) {
+  const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int n = blockIdx.x * 4 + w;
+  __shared__ float s_loss[4];
+  __shared__ int s_cnt[4];
+  float loss = 0.f;
+  int cnt = 0;
+  if (n < N) {
+    float m = kNegBig, s = 0.f;
+    for (int k = l; k < splits; k += 64) {
+      const float m2 = pm[(long)k * N + n], s2 = ps[(long)k * N + n];
+      const float mn = fmaxf(m, m2);
+      s = s * fast_exp2(m - mn) + s2 * fast_exp2(m2 - mn);
+      m = mn;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
+      const float mn = fmaxf(m, m2);
+      s = s * exp2f(m - mn) + s2 * exp2f(m2 - mn);
+      m = mn;
+    }
+    const float lse = m * kLn2 + logf(s + 1e-10f);
+    const long lab = load_label(labels, labels64, n);
+    const bool valid = (lab != ignore_index);
+    float t = 0.f;
+    if (valid && lab >= 0 && lab < V) {
+      const bf16_t* h = H + (long)n * d;
+      const bf16_t* wr = W + lab * (long)d;
+      float dot = 0.f;
+      for (int k = l * 8; k < d; k += 512) {
+        const u32x4 hv = *reinterpret_cast<const u32x4*>(h + k);
+        const u32x4 wv = *reinterpret_cast<const u32x4*>(wr + k);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          dot += bf16_to_f32(hv[q] & 0xffffu) * bf16_to_f32(wv[q] & 0xffffu);
+          dot += bf16_to_f32(hv[q] >> 16) * bf16_to_f32(wv[q] >> 16);
+        }
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o);
+      t = dot + (bias ? bias[lab] : 0.f);
+    }
+    if (valid) {
+      float ce = lse - t;
+      if (eps > 0.f) ce = (1.f - eps) * ce + eps * logV;
+      loss = ce + zw * lse * lse;
+      cnt = 1;
+    }
+    if (l == 0) {
+      lse_out[n] = lse;
+      rowloss[n] = loss;
+    }
+  }
+  if (l == 0) {
+    s_loss[w] = loss;
+    s_cnt[w] = cnt;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    bsum[blockIdx.x] = (s_loss[0] + s_loss[1]) + (s_loss[2] + s_loss[3]);
+    bcnt[blockIdx.x] = s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
+  }
+}
+
+// Single block: fixed-order reduction of the block partials (deterministic).
+__global__ __launch_bounds__(1024) void fwd_finalize_kernel(const float* __restrict__ bsum,
+                                                            const int* __restrict__ bcnt, int nb, int reduction,
+                                                            float* __restrict__ loss_out,
+                                                            int32_t* __restrict__ nvalid_out) {
+  __shared__ float sl[1024];
+  __shared__ int sc[1024];
+  float a = 0.f;
+  int c = 0;
+  for (int i = threadIdx.x; i < nb; i += 1024) {
+    a += bsum[i];
+    c += bcnt[i];
+  }
+  sl[threadIdx.x] = a;
+  sc[threadIdx.x] = c;
+  __syncthreads();
+  for (int o = 512; o >= 1; o >>= 1) {
+    if ((int)threadIdx.x < o) {
+      sl[threadIdx.x] += sl[threadIdx.x + o];
+      sc[threadIdx.x] += sc[threadIdx.x + o];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const int nv = sc[0];
+    nvalid_out[0] = nv;
+    if (reduction == CCE_REDUCTION_MEAN)
+      loss_out[0] = sl[0] / (float)(nv > 1 ? nv : 1);
+    else if (reduction == CCE_REDUCTION_SUM)
+      loss_out[0] = sl[0];
+  }
+}
+
+// Per-row backward coefficients.
+__global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__ grad_out,
+                                                       const float* __restrict__ lse,
+                                                       const int32_t* __restrict__ nvalid, const void* labels,
+                                                       int labels64, int N, int V, long ignore_index, float eps,
+                                                       float zw, int reduction, float4* __restrict__ rowp,
+                                                       int* __restrict__ rowlab) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const long lab = load_label(labels, labels64, n);
+  const bool valid = (lab != ignore_index);
+  float scale = 0.f;
+  if (valid) {
+    const float gsc = (reduction == CCE_REDUCTION_NONE) ? grad_out[n] : grad_out[0];
+    const int nv = nvalid[0];
+    scale = (reduction == CCE_REDUCTION_MEAN) ? gsc / (float)(nv > 1 ? nv : 1) : gsc;
+  }
+  if (valid) {
+    const float L = lse[n];
+    rowp[n] = make_float4(L * kLog2e, scale * (1.f + 2.f * zw * L), scale * (1.f - eps), scale * eps / (float)V);
+    rowlab[n] = (lab >= 0 && lab < V) ? (int)lab : -1;
+  } else {
+    rowp[n] = make_float4(FLT_MAX, 0.f, 0.f, 0.f);
+    rowlab[n] = -1;
+  }
+}
+
+// out[c][r] = in[r][c] for r < R (zero for R <= r < Rpad), c < C.  64x64 tiles.
+__global__ __launch_bounds__(256) void transpose_kernel(const bf16_t* __restrict__ in, long ldi, int R, int C,
+                                                        bf16_t* __restrict__ out, long ldo, int Rpad) {
+  __shared__ bf16_t t[64][66];
+  const int r0 = blockIdx.x * 64, c0 = blockIdx.y * 64;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int q = tid + it * 256;        // 512 chunks of 8 elements
+    const int rr = q >> 3, cc = (q & 7) * 8;
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (r0 + rr < R && c0 + cc < C) v = *reinterpret_cast<const u32x4*>(in + (long)(r0 + rr) * ldi + c0 + cc);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      t[rr][cc + 2 * e] = (bf16_t)(v[e] & 0xffffu);
+      t[rr][cc + 2 * e + 1] = (bf16_t)(v[e] >> 16);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int q = tid + it * 256;
+    const int cc = q >> 3, rr = (q & 7) * 8;
+    if (c0 + cc < C && r0 + rr < Rpad) {
+      u32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (uint32_t)t[rr + 2 * e][cc] | ((uint32_t)t[rr + 2 * e + 1][cc] << 16);
+      *reinterpret_cast<u32x4*>(out + (long)(c0 + cc) * ldo + r0 + rr) = v;
+    }
+  }
+}
+
+// dB[c] = sum_m G[m][c] for c < C (fixed order: deterministic).  Block = 64 columns.
+__global__ __launch_bounds__(256) void colsum_kernel(const bf16_t* __restrict__ G, long ldg, int M, int C,
+                                                     float* __restrict__ out) {
+  __shared__ float part[32][65];
+  const int tid = threadIdx.x;
+  const int cg = tid & 7, rg = tid >> 3;  // 8 column groups of 8, 32 row groups
+  const int c0 = blockIdx.x * 64 + cg * 8;
+  float a[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) a[e] = 0.f;
+  if (c0 < C) {
+    for (int m = rg; m < M; m += 32) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(G + (long)m * ldg + c0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        a[2 * e] += bf16_to_f32(v[e] & 0xffffu);
+        a[2 * e + 1] += bf16_to_f32(v[e] >> 16);
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) part[rg][cg * 8 + e] = a[e];
+  __syncthreads();
+  if (tid < 64) {
+    float s = 0.f;
+    for (int r = 0; r < 32; ++r) s += part[r][tid];
+    const int c = blockIdx.x * 64 + tid;
+    if (c < C) out[c] = s;
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_zero_kernel(uint32_t* __restrict__ p, long nwords) {
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < nwords; i += (long)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                         \
+  do {                                                                                        \
+    hipError_t e_ = (expr);                                                                   \
+    if (e_ != hipSuccess) return fail(CCE_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+inline long ceil_div(long a, long b) { return (a + b - 1) / b; }
+
+struct Carver {
+  char* base;
+  size_t off = 0;
+  explicit Carver(void* p) : base(static_cast<char*>(p)) {}
+  template <class T>
+  T* take(size_t count) {
+    off = align_up(off, 256);
+    T* p = base ? reinterpret_cast<T*>(base + off) : nullptr;
+    off += count * sizeof(T);
+    return p;
+  }
+};
+
+// Forward vocabulary splits: enough (row tile x split) workgroups to cover
+// the 256 CUs several times over.
+int forward_splits(long N, long V) {
+  if (N <= 0) return 1;
+  const long gm = ceil_div(N, kBM), tn = ceil_div(V, 256);
+  long s = ceil_div(2048, gm);
+  if (s > tn) s = tn;
+  if (s < 1) s = 1;
+  return (int)s;
+}
+
+long band_width(long V, long chunk) {
+  long vb = chunk <= 0 ? 8192 : chunk;
+  vb = align_up((size_t)vb, 256);
+  const long vmax = (long)align_up((size_t)V, 256);
+  if (vb > vmax) vb = vmax;
+  if (vb < 256) vb = 256;
+  return vb;
+}
+
+struct FwdLayout {
+  float *pm, *ps, *bsum, *rowloss;
+  int* bcnt;
+  size_t bytes;
+};
+
+FwdLayout fwd_layout(void* ws, long N, long V, int reduction) {
+  Carver c(ws);
+  FwdLayout L;
+  const int S = forward_splits(N, V);
+  const long nb = ceil_div(N, 4);
+  L.pm = c.take<float>((size_t)S * N);
+  L.ps = c.take<float>((size_t)S * N);
+  L.bsum = c.take<float>((size_t)(nb > 0 ? nb : 1));
+  L.bcnt = c.take<int>((size_t)(nb > 0 ? nb : 1));
+  L.rowloss = (reduction == CCE_REDUCTION_NONE) ? nullptr : c.take<float>((size_t)(N > 0 ? N : 1));
+  L.bytes = align_up(c.off, 256);
+  return L;
+}
+
+struct BwdLayout {
+  float4* rowp;
+  int* rowlab;
+  bf16_t* G;
+  bf16_t* WT;
+  bf16_t* HT;
+  float* dHacc;
+  size_t bytes;
+};
+
+BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bool need_dw) {
+  Carver c(ws);
+  BwdLayout L;
+  const long nbands = ceil_div(V, Vb);
+  const long N8 = (long)align_up((size_t)N, 8);
+  L.rowp = c.take<float4>((size_t)N);
+  L.rowlab = c.take<int>((size_t)N);
+  L.G = c.take<bf16_t>((size_t)N * Vb);
+  L.WT = need_dh ? c.take<bf16_t>((size_t)d * Vb) : nullptr;
+  L.HT = need_dw ? c.take<bf16_t>((size_t)d * N8) : nullptr;
+  L.dHacc = (need_dh && nbands > 1) ? c.take<float>((size_t)N * d) : nullptr;
+  L.bytes = align_up(c.off, 256);
+  return L;
+}
+
+bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
+
+int check_dims(long N, long d, long V) {
+  if (N < 0) return fail(CCE_ERR_INVALID_ARG, "N must be >= 0 (got %ld)", N);
+  if (d <= 0 || d % 8 != 0) return fail(CCE_ERR_INVALID_ARG, "hidden dim d must be a positive multiple of 8 (got %ld)", d);
+  if (V <= 0) return fail(CCE_ERR_INVALID_ARG, "vocab size V must be > 0 (got %ld)", V);
+  if (N > (1L << 30) || V > (1L << 30) || d > (1L << 20))
+    return fail(CCE_ERR_INVALID_ARG, "problem too large (N=%ld d=%ld V=%ld)", N, d, V);
+  return CCE_OK;
+}
+
+template <int BN, bool AK, bool BK, template <int> class EpiT>
+int launch_gemm(const GemmShape& g, const typename EpiT<BN>::Params& ep, int nblocks, hipStream_t st) {
+  if (nblocks <= 0) return CCE_OK;
+  hipLaunchKernelGGL((gemm_kernel<BN, AK, BK, EpiT>), dim3(nblocks), dim3(kThreads), 0, st, g, ep);
+  HIP_TRY(hipGetLastError());
+  return CCE_OK;
+}
+
+int zero_fill(void* p, size_t bytes, hipStream_t st) {
+  if (!p || bytes == 0) return CCE_OK;
+  const long words = (long)(bytes / 4);
+  long blocks = ceil_div(words, 256);
+  if (blocks > 4096) blocks = 4096;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, st, reinterpret_cast<uint32_t*>(p),
+                     words);
+  HIP_TRY(hipGetLastError());
+  return CCE_OK;
+}
+
+// Band GEMM for dH / dW: pick the column tile that wastes least of d.
+bool use_bn256(long d) { return (align_up((size_t)d, 256) - d) <= (align_up((size_t)d, 128) - d); }
+
+template <int BN>
+int launch_dh(const GemmShape& g, const EpiAcc<256>::Params& ep, hipStream_t st) {
+  const int nb = (int)(ceil_div(g.M, kBM) * ceil_div(g.N, BN));
+  typename EpiAcc<BN>::Params p;
+  p.acc32 = ep.acc32; p.ldacc = ep.ldacc; p.out = ep.out; p.ldo = ep.ldo; p.out_f32 = ep.out_f32; p.mode = ep.mode;
+  return launch_gemm<BN, true, true, EpiAcc>(g, p, nb, st);
+}
+
+template <int BN>
+int launch_dw(const GemmShape& g, const EpiAcc<256>::Params& ep, hipStream_t st) {
+  const int nb = (int)(ceil_div(g.M, kBM) * ceil_div(g.N, BN));
+  typename EpiAcc<BN>::Params p;
+  p.acc32 = ep.acc32; p.ldacc = ep.ldacc; p.out = ep.out; p.ldo = ep.ldo; p.out_f32 = ep.out_f32; p.mode = ep.mode;
+  return launch_gemm<BN, false, true, EpiAcc>(g, p, nb, st);
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+
+extern "C" {
+
+const char* cce_last_error(void) { return g_err; }
+
+int cce_abi_version(void) { return CCE_ABI_VERSION; }
+
+int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, size_t* bytes) {
+  g_err[0] = 0;
+  if (!bytes) return fail(CCE_ERR_INVALID_ARG, "bytes must not be null");
+  int rc = check_dims(N, d, V);
+  if (rc) return rc;
+  if (reduction < CCE_REDUCTION_NONE || reduction > CCE_REDUCTION_SUM)
+    return fail(CCE_ERR_INVALID_ARG, "reduction must be 0 (none), 1 (mean) or 2 (sum), got %d", reduction);
+  *bytes = fwd_layout(nullptr, N, V, reduction).bytes;
+  return CCE_OK;
+}
+
+int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_size, int need_grad_hidden,
+                                 int need_grad_weight, size_t* bytes) {
+  g_err[0] = 0;
+  if (!bytes) return fail(CCE_ERR_INVALID_ARG, "bytes must not be null");
+  int rc = check_dims(N, d, V);
+  if (rc) return rc;
+  *bytes = bwd_layout(nullptr, N, d, V, band_width(V, chunk_size), need_grad_hidden != 0, need_grad_weight != 0).bytes;
+  return CCE_OK;
+}
+
+int cce_forward(const void* hidden, const void* weight, const void* labels, int labels_int64, const float* bias,
+                int64_t N, int64_t d, int64_t V, int64_t ignore_index, float label_smoothing, float z_loss_weight,
+                int reduction, float* loss_out, float* lse_out, int32_t* n_valid_out, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = check_dims(N, d, V);
+  if (rc) return rc;
+  if (reduction < CCE_REDUCTION_NONE || reduction > CCE_REDUCTION_SUM)
+    return fail(CCE_ERR_INVALID_ARG, "reduction must be 0 (none), 1 (mean) or 2 (sum), got %d", reduction);
+  if (!n_valid_out || (!loss_out && !(reduction == CCE_REDUCTION_NONE && N == 0)))
+    return fail(CCE_ERR_INVALID_ARG, "loss_out and n_valid_out must not be null");
+  if (N > 0 && (!hidden || !weight || !labels || !lse_out))
+    return fail(CCE_ERR_INVALID_ARG, "hidden, weight, labels and lse_out must not be null");
+  if (!(label_smoothing >= 0.f && label_smoothing <= 1.f))
+    return fail(CCE_ERR_INVALID_ARG, "label_smoothing must be in [0, 1]");
+  if (misaligned(hidden) || misaligned(weight) || misaligned(workspace))
+    return fail(CCE_ERR_INVALID_ARG, "hidden, weight and workspace must be 16-byte aligned");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const FwdLayout need = fwd_layout(nullptr, N, V, reduction);
+  if (workspace_bytes < need.bytes || (need.bytes && !workspace))
+    return fail(CCE_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need.bytes, workspace_bytes);
+  if (N == 0) {
+    rc = zero_fill(n_valid_out, sizeof(int32_t), st);
+    if (!rc && reduction != CCE_REDUCTION_NONE) rc = zero_fill(loss_out, sizeof(float), st);
+    return rc;
+  }
+  const FwdLayout L = fwd_layout(workspace, N, V, reduction);
+  const int S = forward_splits(N, V);
+  const int gm = (int)ceil_div(N, kBM);
+
+  GemmShape g;
+  g.A = static_cast<const bf16_t*>(hidden);
+  g.lda = d;
+  g.B = static_cast<const bf16_t*>(weight);
+  g.ldb = d;
+  g.M = (int)N;
+  g.N = (int)V;
+  g.K = (int)d;
+  EpiLse<256>::Params ep;
+  ep.bias = bias;
+  ep.pm = L.pm;
+  ep.ps = L.ps;
+  ep.splits = S;
+  ep.tiles_n = (int)ceil_div(V, 256);
+  rc = launch_gemm<256, true, true, EpiLse>(g, ep, gm * S, st);
+  if (rc) return rc;
+
+  const int nb = (int)ceil_div(N, 4);
+  float* rowloss = (reduction == CCE_REDUCTION_NONE) ? loss_out : L.rowloss;
+  const float logV = logf((float)V);
+  hipLaunchKernelGGL(fwd_combine_kernel, dim3(nb), dim3(256), 0, st, L.pm, L.ps, S,
+                     static_cast<const bf16_t*>(hidden), static_cast<const bf16_t*>(weight), labels, labels_int64,
+                     bias, (int)N, (int)d, (int)V, (long)ignore_index, label_smoothing, z_loss_weight, logV, lse_out,
+                     rowloss, L.bsum, L.bcnt);
+  HIP_TRY(hipGetLastError());
+  hipLaunchKernelGGL(fwd_finalize_kernel, dim3(1), dim3(1024), 0, st, L.bsum, L.bcnt, nb, reduction, loss_out,
+                     n_valid_out);
+  HIP_TRY(hipGetLastError());
+  return CCE_OK;
+}
+
+int cce_backward(const float* grad_out, const void* hidden, const void* weight, const void* labels, int labels_int64,
+                 const float* bias, const float* lse, const int32_t* n_valid, int64_t N, int64_t d, int64_t V,
+                 int64_t ignore_index, float label_smoothing, float z_loss_weight, int reduction, int64_t chunk_size,
+                 void* grad_hidden, int grad_hidden_dtype, void* grad_weight, int grad_weight_dtype,
+                 float* grad_bias, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = check_dims(N, d, V);
+  if (rc) return rc;
+  if (reduction < CCE_REDUCTION_NONE || reduction > CCE_REDUCTION_SUM)
+    return fail(CCE_ERR_INVALID_ARG, "reduction must be 0 (none), 1 (mean) or 2 (sum), got %d", reduction);
+  if ((grad_hidden && grad_hidden_dtype != CCE_DTYPE_BF16 && grad_hidden_dtype != CCE_DTYPE_F32) ||
+      (grad_weight && grad_weight_dtype != CCE_DTYPE_BF16 && grad_weight_dtype != CCE_DTYPE_F32))
+    return fail(CCE_ERR_INVALID_ARG, "gradient dtypes must be CCE_DTYPE_BF16 or CCE_DTYPE_F32");
+  if (N > 0 && (!grad_out || !hidden || !weight || !labels || !lse || !n_valid))
+    return fail(CCE_ERR_INVALID_ARG, "grad_out, hidden, weight, labels, lse and n_valid must not be null");
+  if (!(label_smoothing >= 0.f && label_smoothing <= 1.f))
+    return fail(CCE_ERR_INVALID_ARG, "label_smoothing must be in [0, 1]");
+  if (misaligned(hidden) || misaligned(weight) || misaligned(workspace) || misaligned(grad_hidden) ||
+      misaligned(grad_weight))
+    return fail(CCE_ERR_INVALID_ARG, "hidden, weight, gradients and workspace must be 16-byte aligned");
+  const bool need_dh = grad_hidden != nullptr, need_dw = grad_weight != nullptr, need_db = grad_bias != nullptr;
+  if (need_db && !bias) return fail(CCE_ERR_INVALID_ARG, "grad_bias requested without bias");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const long Vb = band_width(V, chunk_size);
+  const BwdLayout need = bwd_layout(nullptr, N, d, V, Vb, need_dh, need_dw);
+  if (workspace_bytes < need.bytes || (need.bytes && !workspace))
+    return fail(CCE_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need.bytes, workspace_bytes);
+  if (N == 0) {
+    if (need_dw) {
+      rc = zero_fill(grad_weight, (size_t)V * d * (grad_weight_dtype == CCE_DTYPE_F32 ? 4 : 2), st);
+      if (rc) return rc;
+    }
+    if (need_db) return zero_fill(grad_bias, (size_t)V * 4, st);
+    return CCE_OK;
+  }
+  if (!need_dh && !need_dw && !need_db) return CCE_OK;
+  const BwdLayout L = bwd_layout(workspace, N, d, V, Vb, need_dh, need_dw);
+  const long N8 = (long)align_up((size_t)N, 8);
+  const bf16_t* H = static_cast<const bf16_t*>(hidden);
+  const bf16_t* W = static_cast<const bf16_t*>(weight);
+
+  hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)ceil_div(N, 256)), dim3(256), 0, st, grad_out, lse, n_valid,
+                     labels, labels_int64, (int)N, (int)V, (long)ignore_index, label_smoothing, z_loss_weight,
+                     reduction, L.rowp, L.rowlab);
+  HIP_TRY(hipGetLastError());
+  if (need_dw) {
+    hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)ceil_div(N8, 64), (unsigned)ceil_div(d, 64)), dim3(256), 0,
+                       st, H, (long)d, (int)N, (int)d, L.HT, (long)N8, (int)N8);
+    HIP_TRY(hipGetLastError());
+  }
+
+  const long nbands = ceil_div(V, Vb);
+  const int gm = (int)ceil_div(N, kBM);
+  for (long b = 0; b < nbands; ++b) {
+    const long v0 = b * Vb;
+    const long vb = (V - v0 < Vb) ? (V - v0) : Vb;
+    const long vb64 = (long)align_up((size_t)vb, 64);
+
+    // G = dLoss/dS for columns [v0, v0 + vb)
+    GemmShape g1;
+    g1.A = H; g1.lda = d; g1.B = W + v0 * d; g1.ldb = d;
+    g1.M = (int)N; g1.N = (int)vb; g1.K = (int)d;
+    EpiGrad<256>::Params e1;
+    e1.bias = bias; e1.rowp = L.rowp; e1.rowlab = L.rowlab; e1.G = L.G; e1.ldg = Vb; e1.v0 = (int)v0;
+    rc = launch_gemm<256, true, true, EpiGrad>(g1, e1, gm * (int)ceil_div(vb, 256), st);
+    if (rc) return rc;
+
+    if (need_dh) {
+      // WT[j][c] = W[v0 + c][j], zero for vb <= c < vb64
+      hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)ceil_div(vb64, 64), (unsigned)ceil_div(d, 64)), dim3(256),
+                         0, st, W + v0 * d, (long)d, (int)vb, (int)d, L.WT, (long)Vb, (int)vb64);
+      HIP_TRY(hipGetLastError());
+      GemmShape g2;
+      g2.A = L.G; g2.lda = Vb; g2.B = L.WT; g2.ldb = Vb;
+      g2.M = (int)N; g2.N = (int)d; g2.K = (int)vb64;
+      EpiAcc<256>::Params e2;
+      e2.acc32 = L.dHacc; e2.ldacc = d; e2.out = grad_hidden; e2.ldo = d;
+      e2.out_f32 = (grad_hidden_dtype == CCE_DTYPE_F32);
+      e2.mode = (nbands == 1) ? 0 : (b == 0 ? 1 : (b == nbands - 1 ? 3 : 2));
+      rc = use_bn256(d) ? launch_dh<256>(g2, e2, st) : launch_dh<128>(g2, e2, st);
+      if (rc) return rc;
+    }
+    if (need_dw) {
+      GemmShape g3;
+      g3.A = L.G; g3.lda = Vb;  // MN-major: element (v, n) at G[n*Vb + v]
+      g3.B = L.HT; g3.ldb = N8;
+      g3.M = (int)vb; g3.N = (int)d; g3.K = (int)N;
+      EpiAcc<256>::Params e3;
+      e3.acc32 = nullptr; e3.ldacc = 0;
+      e3.out = (grad_weight_dtype == CCE_DTYPE_F32)
+                   ? static_cast<void*>(static_cast<float*>(grad_weight) + v0 * d)
+                   : static_cast<void*>(static_cast<bf16_t*>(grad_weight) + v0 * d);
+      e3.ldo = d;
+      e3.out_f32 = (grad_weight_dtype == CCE_DTYPE_F32);
+      e3.mode = 0;
+      rc = use_bn256(d) ? launch_dw<256>(g3, e3, st) : launch_dw<128>(g3, e3, st);
+      if (rc) return rc;
+    }
+    if (need_db) {
+      hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)ceil_div(vb, 64)), dim3(256), 0, st, L.G, (long)Vb, (int)N,
+                         (int)vb, grad_bias + v0);
+      HIP_TRY(hipGetLastError());
+    }
+  }
+  return CCE_OK;
+}
+
+}  // extern "C"

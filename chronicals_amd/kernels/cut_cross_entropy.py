@@ -1,0 +1,304 @@
+"""Cut Cross-Entropy (fused lm_head projection + cross-entropy) on MI355X.
+
+Drop-in for ``chronicals.kernels.cut_cross_entropy`` (reference
+chronicals/kernels/cut_cross_entropy.py): same public names, argument order,
+defaults and loss semantics, with the compute in hand-written gfx950 HIP
+kernels (``libchronicals_cce.so``, C ABI in include/chronicals_cce.h).
+
+Differences from the reference, all deliberate:
+  * ``reduction`` keyword ('mean' | 'sum' | 'none'), with the semantics of the
+    reference's sibling ``fused_linear_cross_entropy``
+    (triton_kernels.py:2481-2491).  ``CutCrossEntropyLoss`` accepts all three
+    (the reference raises for anything but 'mean', cut_cross_entropy.py:1120).
+  * The backward applies the one-hot term of dLoss/dlogits, which the
+    reference's CPU backward loses (cut_cross_entropy.py:773-780); its GPU path
+    (:530-546) applies it.
+  * Tensors must live on a HIP device; there is no CPU path.  hidden and weight
+    are computed in bf16 with fp32 accumulation (fp16/fp32 inputs are rounded
+    to bf16 at the boundary); gradients come back in the input dtypes (:808).
+  * ``use_triton`` is accepted and ignored: there is one HIP path.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from .. import _lib
+
+# Constants of the reference module (cut_cross_entropy.py:45-56), kept for
+# import compatibility.  The chunk size is the vocabulary band width of the
+# backward pass here.
+CHUNK_SIZE_SMALL_VOCAB = 4096
+CHUNK_SIZE_MEDIUM_VOCAB = 8192
+CHUNK_SIZE_LARGE_VOCAB = 16384
+DEFAULT_VOCAB_CHUNK_SIZE = 8192
+TRITON_BLOCK_SIZE = 4096
+TRITON_BLOCK_SIZE_MAX = 65536 // 2
+
+__all__ = [
+    "cut_cross_entropy",
+    "CutCrossEntropyLoss",
+    "CutCrossEntropyFunction",
+    "get_optimal_chunk_size",
+    "estimate_memory_savings",
+    "compute_z_loss",
+]
+
+
+def get_optimal_chunk_size(vocab_size: int, hidden_dim: int, available_vram_gb: float = 40.0) -> int:
+    """Power-of-two vocabulary chunk for a vocabulary size.
+
+    Same rule as the reference (cut_cross_entropy.py:59-90): 4096 below 64K
+    entries, 8192 below 128K, 16384 above, capped by 80% of
+    ``available_vram_gb`` over 8*hidden_dim bytes per entry, at least 256.
+    """
+    usable = available_vram_gb * 0.8 * 1024 ** 3
+    max_chunk = int(usable / (8 * hidden_dim))
+    if vocab_size < 64000:
+        optimal = min(max_chunk, CHUNK_SIZE_SMALL_VOCAB)
+    elif vocab_size < 128000:
+        optimal = min(max_chunk, CHUNK_SIZE_MEDIUM_VOCAB)
+    else:
+        optimal = min(max_chunk, CHUNK_SIZE_LARGE_VOCAB)
+    return max(256, 2 ** int(math.log2(optimal)))
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _as_bf16_rows(x: torch.Tensor) -> torch.Tensor:
+    """Contiguous, 16-byte aligned bf16 copy/view of a 2-D tensor."""
+    if x.dtype != torch.bfloat16:
+        x = x.to(torch.bfloat16)
+    if not x.is_contiguous() or x.data_ptr() % 16 != 0:
+        x = x.contiguous()
+        if x.data_ptr() % 16 != 0:
+            x = x.clone()
+    return x
+
+
+def _validate(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor, bias: Optional[torch.Tensor]):
+    if not (hidden.is_cuda and weight.is_cuda and labels.is_cuda):
+        raise RuntimeError(
+            "chronicals_amd cut_cross_entropy runs only on HIP devices: hidden, weight and labels must be "
+            f"device tensors (got {hidden.device}, {weight.device}, {labels.device})"
+        )
+    if hidden.device != weight.device or hidden.device != labels.device:
+        raise RuntimeError("hidden, weight and labels must be on the same device")
+    if weight.dim() != 2:
+        raise RuntimeError(f"weight must be [vocab_size, hidden_dim], got shape {tuple(weight.shape)}")
+    if hidden.dim() < 1 or hidden.shape[-1] != weight.shape[1]:
+        raise RuntimeError(
+            f"hidden last dim {tuple(hidden.shape)[-1:]} does not match weight hidden_dim {weight.shape[1]}"
+        )
+    if labels.dtype not in (torch.int64, torch.int32):
+        raise RuntimeError(f"labels must be int64 or int32, got {labels.dtype}")
+    n = hidden.numel() // hidden.shape[-1] if hidden.shape[-1] else 0
+    if labels.numel() != n:
+        raise RuntimeError(f"labels has {labels.numel()} elements but hidden has {n} rows")
+    if bias is not None:
+        if bias.dim() != 1 or bias.shape[0] != weight.shape[0]:
+            raise RuntimeError(f"bias must be [vocab_size={weight.shape[0]}], got {tuple(bias.shape)}")
+        if bias.device != hidden.device:
+            raise RuntimeError("bias must be on the same device as hidden")
+    if hidden.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise RuntimeError(f"hidden dtype {hidden.dtype} not supported (bf16, fp16, fp32)")
+    if weight.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise RuntimeError(f"weight dtype {weight.dtype} not supported (bf16, fp16, fp32)")
+
+
+def _reduction_code(reduction: str) -> int:
+    try:
+        return _lib.REDUCTIONS[reduction]
+    except KeyError:
+        raise ValueError(f"reduction must be 'mean', 'sum' or 'none', got {reduction!r}") from None
+
+
+def _forward_raw(hidden, weight, labels, bias, ignore_index, label_smoothing, z_loss_weight, red):
+    """One cce_forward call.  Returns (loss, lse, n_valid, h2, w2, lab, b32)."""
+    lib = _lib.load()
+    _validate(hidden, weight, labels, bias)
+    device = hidden.device
+    d = hidden.shape[-1]
+    V = weight.shape[0]
+    h2 = _as_bf16_rows(hidden.detach().reshape(-1, d))
+    w2 = _as_bf16_rows(weight.detach())
+    N = h2.shape[0]
+    lab = labels.reshape(-1)
+    if not lab.is_contiguous():
+        lab = lab.contiguous()
+    b32 = None if bias is None else bias.detach().to(torch.float32).contiguous()
+    with torch.cuda.device(device):
+        ws = torch.empty(_lib.forward_workspace_bytes(N, d, V, red), dtype=torch.uint8, device=device)
+        loss = torch.empty((N,) if red == _lib.CCE_REDUCTION_NONE else (1,), dtype=torch.float32, device=device)
+        lse = torch.empty((N,), dtype=torch.float32, device=device)
+        n_valid = torch.empty((1,), dtype=torch.int32, device=device)
+        _lib.check(lib.cce_forward(
+            h2.data_ptr(), w2.data_ptr(), lab.data_ptr(), int(lab.dtype == torch.int64),
+            b32.data_ptr() if b32 is not None else None,
+            N, d, V, int(ignore_index), float(label_smoothing), float(z_loss_weight), red,
+            loss.data_ptr(), lse.data_ptr(), n_valid.data_ptr(),
+            ws.data_ptr(), ws.numel(), _stream_handle(device)))
+    return loss, lse, n_valid, h2, w2, lab, b32
+
+
+class CutCrossEntropyFunction(torch.autograd.Function):
+    """Autograd contract of the reference (cut_cross_entropy.py:815-858).
+
+    forward(hidden, weight, labels, bias, chunk_size, ignore_index,
+            label_smoothing, z_loss_weight, reduction) -> loss
+    Saves only the bf16 operands, labels, lse [N] and n_valid (O(N) extra).
+    """
+
+    @staticmethod
+    def forward(ctx, hidden, weight, labels, bias, chunk_size, ignore_index, label_smoothing, z_loss_weight,
+                reduction="mean"):
+        red = _reduction_code(reduction)
+        loss, lse, n_valid, h2, w2, lab, b32 = _forward_raw(hidden, weight, labels, bias, ignore_index,
+                                                            label_smoothing, z_loss_weight, red)
+        ctx.save_for_backward(h2, w2, lab, lse, n_valid, b32)
+        ctx.cfg = (int(chunk_size), int(ignore_index), float(label_smoothing), float(z_loss_weight), red)
+        ctx.shapes = (hidden.shape, hidden.dtype, weight.dtype, None if bias is None else bias.dtype)
+        if red == _lib.CCE_REDUCTION_NONE:
+            return loss.view(labels.shape)
+        return loss.view(())
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        lib = _lib.load()
+        h2, w2, lab, lse, n_valid, b32 = ctx.saved_tensors
+        chunk_size, ignore_index, eps, zw, red = ctx.cfg
+        hshape, hdtype, wdtype, bdtype = ctx.shapes
+        need_dh = ctx.needs_input_grad[0]
+        need_dw = ctx.needs_input_grad[1]
+        need_db = b32 is not None and ctx.needs_input_grad[3]
+        if not (need_dh or need_dw or need_db):
+            return (None,) * 9
+        device = h2.device
+        N, d = h2.shape
+        V = w2.shape[0]
+        g = grad_output.detach().to(torch.float32).reshape(-1).contiguous()
+        with torch.cuda.device(device):
+            dh = dw = db = None
+            if need_dh:
+                dh = torch.empty((N, d), dtype=torch.bfloat16 if hdtype == torch.bfloat16 else torch.float32,
+                                 device=device)
+            if need_dw:
+                dw = torch.empty((V, d), dtype=torch.bfloat16 if wdtype == torch.bfloat16 else torch.float32,
+                                 device=device)
+            if need_db:
+                db = torch.empty((V,), dtype=torch.float32, device=device)
+            ws = torch.empty(_lib.backward_workspace_bytes(N, d, V, chunk_size, need_dh, need_dw),
+                             dtype=torch.uint8, device=device)
+            _lib.check(lib.cce_backward(
+                g.data_ptr(), h2.data_ptr(), w2.data_ptr(), lab.data_ptr(), int(lab.dtype == torch.int64),
+                b32.data_ptr() if b32 is not None else None, lse.data_ptr(), n_valid.data_ptr(),
+                N, d, V, ignore_index, eps, zw, red, chunk_size,
+                dh.data_ptr() if dh is not None else None,
+                _lib.CCE_DTYPE_BF16 if (dh is not None and dh.dtype == torch.bfloat16) else _lib.CCE_DTYPE_F32,
+                dw.data_ptr() if dw is not None else None,
+                _lib.CCE_DTYPE_BF16 if (dw is not None and dw.dtype == torch.bfloat16) else _lib.CCE_DTYPE_F32,
+                db.data_ptr() if db is not None else None,
+                ws.data_ptr(), ws.numel(), _stream_handle(device)))
+        if dh is not None:
+            dh = dh.view(hshape).to(hdtype)
+        if dw is not None:
+            dw = dw.to(wdtype)
+        if db is not None:
+            db = db.to(bdtype)
+        return dh, dw, None, db, None, None, None, None, None
+
+
+def cut_cross_entropy(
+    hidden: torch.Tensor,
+    weight: torch.Tensor,
+    labels: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+    chunk_size: int = 8192,
+    ignore_index: int = -100,
+    label_smoothing: float = 0.0,
+    z_loss_weight: float = 0.0,
+    use_triton: bool = True,
+    reduction: str = "mean",
+) -> torch.Tensor:
+    """Fused lm_head projection + cross-entropy without materialising logits.
+
+    Signature and defaults of the reference (cut_cross_entropy.py:1023-1033)
+    plus ``reduction``.  hidden [B,S,d] or [N,d]; weight [V,d]; labels [B,S]
+    or [N] (int64/int32); bias [V] or None.  Returns a 0-dim fp32 loss for
+    'mean'/'sum' and a labels-shaped fp32 tensor for 'none'.  The loss of a
+    row is (1-eps)*(lse - target) + eps*log(V) + z*lse^2 (reference
+    :671-683); rows labelled ``ignore_index`` contribute 0 and are excluded
+    from the mean's denominator max(n_valid, 1) (:686-690).
+    """
+    del use_triton  # single HIP path
+    return CutCrossEntropyFunction.apply(hidden, weight, labels, bias, chunk_size, ignore_index, label_smoothing,
+                                         z_loss_weight, reduction)
+
+
+class CutCrossEntropyLoss(nn.Module):
+    """nn.Module wrapper (reference cut_cross_entropy.py:1081-1162).
+
+    ``chunk_size=None`` picks ``get_optimal_chunk_size(V, d)`` per call, as
+    the reference does (:1143-1146).  Accepts reduction 'mean', 'sum' or
+    'none'.
+    """
+
+    def __init__(self, chunk_size: Optional[int] = None, ignore_index: int = -100, label_smoothing: float = 0.0,
+                 z_loss_weight: float = 0.0, reduction: str = "mean"):
+        super().__init__()
+        _reduction_code(reduction)
+        self.chunk_size = chunk_size
+        self.ignore_index = ignore_index
+        self.label_smoothing = label_smoothing
+        self.z_loss_weight = z_loss_weight
+        self.reduction = reduction
+
+    def forward(self, hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
+                bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if self.chunk_size is None:
+            chunk_size = get_optimal_chunk_size(weight.shape[0], weight.shape[1])
+        else:
+            chunk_size = self.chunk_size
+        return cut_cross_entropy(hidden, weight, labels, bias, chunk_size, self.ignore_index, self.label_smoothing,
+                                 self.z_loss_weight, reduction=self.reduction)
+
+    def extra_repr(self) -> str:
+        return (f"chunk_size={self.chunk_size}, ignore_index={self.ignore_index}, "
+                f"label_smoothing={self.label_smoothing}, z_loss_weight={self.z_loss_weight}")
+
+
+def compute_z_loss(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
+                   bias: Optional[torch.Tensor] = None, ignore_index: int = -100,
+                   chunk_size: int = 8192) -> torch.Tensor:
+    """Mean over valid rows of lse^2 (reference cut_cross_entropy.py:1379-1400).
+
+    Not differentiable (the reference's is not either: it runs the forward
+    pass only).  ``chunk_size`` is accepted for signature compatibility.
+    """
+    del chunk_size
+    _, lse, _, _, _, lab, _ = _forward_raw(hidden, weight, labels, bias, ignore_index, 0.0, 0.0,
+                                           _lib.CCE_REDUCTION_NONE)
+    valid = (lab != ignore_index).to(torch.float32)
+    return (lse * lse * valid).sum() / valid.sum().clamp(min=1)
+
+
+def estimate_memory_savings(batch_size: int, seq_len: int, vocab_size: int, chunk_size: int = 8192) -> dict:
+    """Analytic MB estimate of the reference (cut_cross_entropy.py:1403-1430).
+
+    Standard = N*V*4*2 bytes (fp32 logits and their gradient); chunked =
+    N*chunk*4*2 bytes.
+    """
+    batch_seq = batch_size * seq_len
+    standard_mb = batch_seq * vocab_size * 4 * 2 / (1024 ** 2)
+    cce_mb = batch_seq * chunk_size * 4 * 2 / (1024 ** 2)
+    return {
+        "standard_mb": standard_mb,
+        "cce_mb": cce_mb,
+        "reduction_factor": standard_mb / cce_mb,
+        "savings_mb": standard_mb - cce_mb,
+    }

@@ -1,0 +1,113 @@
+/*
+ * chronicals_cce.h — C ABI of the MI355X (gfx950) fused linear cross-entropy
+ * ("Cut Cross-Entropy") library, libchronicals_cce.so.
+ *
+ * The reference (Ajwebdevs/Chronicals v0.1.4) exposes this path as Python:
+ *   chronicals/kernels/cut_cross_entropy.py:1023  cut_cross_entropy(...)
+ *   chronicals/kernels/cut_cross_entropy.py:815   CutCrossEntropyFunction (autograd)
+ *   chronicals/kernels/cut_cross_entropy.py:567   CutCrossEntropyForward.forward
+ *   chronicals/kernels/cut_cross_entropy.py:703   CutCrossEntropyBackward.backward
+ * and has no native library of its own; the entry points below are what a
+ * ctypes/torch-extension binding of those two static methods needs: plain
+ * device pointers, sizes and a HIP stream, no torch types.
+ *
+ * Conventions
+ *   - hidden  [N][d] and weight [V][d] are row-major bf16 (raw 16-bit words),
+ *     16-byte aligned, d a multiple of 8.  All arithmetic accumulates in fp32.
+ *   - labels [N] are int64 (labels_int64 = 1) or int32 (labels_int64 = 0).
+ *     A row whose label equals ignore_index contributes nothing; a label
+ *     outside [0, V) that is not ignore_index has no target logit (loss = lse),
+ *     as in the reference (cut_cross_entropy.py:663-668).
+ *   - bias is an optional fp32 [V] vector (NULL for none).
+ *   - Every call enqueues work on `stream` (a hipStream_t; NULL = default
+ *     stream) and returns without synchronising.  Results are deterministic:
+ *     no floating-point atomics are used.
+ *   - Scratch memory is supplied by the caller (`workspace`), sized by the
+ *     *_workspace_bytes queries; the library allocates no device memory.
+ *   - Return value 0 = success; otherwise a CCE_ERR_* code, with a message
+ *     from cce_last_error() (thread-local).
+ */
+#ifndef CHRONICALS_CCE_H
+#define CHRONICALS_CCE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CCE_ABI_VERSION 1
+
+#define CCE_OK 0
+#define CCE_ERR_INVALID_ARG 1
+#define CCE_ERR_WORKSPACE 2
+#define CCE_ERR_HIP 3
+
+/* reduction: 'none' / 'mean' / 'sum' (triton_kernels.py:2481-2491) */
+#define CCE_REDUCTION_NONE 0
+#define CCE_REDUCTION_MEAN 1
+#define CCE_REDUCTION_SUM 2
+
+/* gradient output element types */
+#define CCE_DTYPE_BF16 0
+#define CCE_DTYPE_F32 1
+
+/* Library ABI version (CCE_ABI_VERSION).  No reference counterpart. */
+int cce_abi_version(void);
+
+/* Message for the last non-zero return on this thread. */
+const char* cce_last_error(void);
+
+/* Workspace bytes cce_forward needs for this problem. */
+int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, size_t* bytes);
+
+/*
+ * Forward.  Replaces CutCrossEntropyForward.forward
+ * (chronicals/kernels/cut_cross_entropy.py:567-692) plus the reduction of
+ * fused_linear_cross_entropy (chronicals/kernels/triton_kernels.py:2481-2491):
+ *   lse[n]   = logsumexp_v (hidden[n] . weight[v] + bias[v])         (:627-671)
+ *   row[n]   = valid ? (1-eps)*(lse - t) + eps*log(V) + z*lse^2 : 0  (:674-686)
+ *   loss_out = mean: sum(row)/max(n_valid,1); sum: sum(row); none: row[N]
+ *   n_valid_out[0] = number of rows with label != ignore_index        (:618, :689)
+ * lse_out [N] fp32 is what cce_backward consumes (the reference saves it at
+ * :841).  loss_out holds 1 float (mean/sum) or N floats (none).
+ */
+int cce_forward(const void* hidden, const void* weight, const void* labels, int labels_int64,
+                const float* bias, int64_t N, int64_t d, int64_t V, int64_t ignore_index,
+                float label_smoothing, float z_loss_weight, int reduction, float* loss_out,
+                float* lse_out, int32_t* n_valid_out, void* workspace, size_t workspace_bytes,
+                void* stream);
+
+/* Workspace bytes cce_backward needs (chunk_size = vocabulary band width). */
+int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_size,
+                                 int need_grad_hidden, int need_grad_weight, size_t* bytes);
+
+/*
+ * Backward.  Replaces CutCrossEntropyBackward.backward
+ * (chronicals/kernels/cut_cross_entropy.py:703-808) with the one-hot term
+ * applied (as the reference's GPU path, :530-546, and
+ * triton_kernels.py:2594-2601 do; its CPU path loses it at :773-780):
+ *   G[n][v] = (P - (1-eps)*onehot - eps/V + 2z*lse*P) * valid * g_n
+ *   g_n     = grad_out[0]/max(n_valid,1) (mean), grad_out[0] (sum), grad_out[n] (none)
+ *   grad_hidden = G . weight  [N][d]    (:795)
+ *   grad_weight = G^T . hidden [V][d]   (:798)
+ *   grad_bias   = sum_n G      [V]      (:801-802)
+ * Any of grad_hidden / grad_weight / grad_bias may be NULL to skip it (a
+ * frozen lm_head skips grad_weight, as triton_kernels.py:3213 does).
+ * grad_*_dtype selects CCE_DTYPE_BF16 or CCE_DTYPE_F32 output; grad_bias is
+ * fp32.  The vocabulary is processed in bands of chunk_size columns (rounded
+ * up to a multiple of 256), the reference's chunk_size argument (:1028).
+ */
+int cce_backward(const float* grad_out, const void* hidden, const void* weight, const void* labels,
+                 int labels_int64, const float* bias, const float* lse, const int32_t* n_valid,
+                 int64_t N, int64_t d, int64_t V, int64_t ignore_index, float label_smoothing,
+                 float z_loss_weight, int reduction, int64_t chunk_size, void* grad_hidden,
+                 int grad_hidden_dtype, void* grad_weight, int grad_weight_dtype, float* grad_bias,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CHRONICALS_CCE_H */

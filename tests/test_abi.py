@@ -1,0 +1,143 @@
+"""The C-ABI library loads and exports every entry point include/*.h declares.
+
+Runs without a GPU: only host-side entry points (version, workspace queries,
+argument validation that returns before any HIP call) are invoked.
+"""
+import ctypes
+import glob
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from chronicals_amd import _lib
+from chronicals_amd import build as _build
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+DECL = re.compile(r"^\s*(?:const\s+)?[A-Za-z_][\w]*\s*\**\s+\**\s*(cce_\w+)\s*\(", re.M)
+
+
+def declared_functions():
+    names = set()
+    for hdr in glob.glob(os.path.join(REPO, "include", "*.h")):
+        names.update(DECL.findall(open(hdr).read()))
+    return names
+
+
+def header_define(name):
+    for hdr in glob.glob(os.path.join(REPO, "include", "*.h")):
+        m = re.search(rf"#define\s+{name}\s+(\d+)", open(hdr).read())
+        if m:
+            return int(m.group(1))
+    raise KeyError(name)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.lib_path()):
+        pytest.fail(f"{_lib.lib_path()} is not built: run __graft_entry__.build()")
+    return _lib.load()
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    for n in ("cce_forward", "cce_backward", "cce_forward_workspace_bytes", "cce_backward_workspace_bytes",
+              "cce_last_error", "cce_abi_version"):
+        assert n in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in sorted(declared_functions()):
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+    assert set(_lib.SIGNATURES) <= declared_functions()
+
+
+def test_no_undeclared_exports():
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", "--defined-only", _lib.lib_path()], capture_output=True, text=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if ln.split() and ln.split()[-1].startswith("cce_")}
+    assert exported == declared_functions()
+
+
+def test_constants_match_header():
+    for name in ("CCE_ABI_VERSION", "CCE_OK", "CCE_ERR_INVALID_ARG", "CCE_ERR_WORKSPACE", "CCE_ERR_HIP",
+                 "CCE_REDUCTION_NONE", "CCE_REDUCTION_MEAN", "CCE_REDUCTION_SUM", "CCE_DTYPE_BF16",
+                 "CCE_DTYPE_F32"):
+        assert getattr(_lib, name) == header_define(name), name
+
+
+def test_abi_version(lib):
+    assert lib.cce_abi_version() == header_define("CCE_ABI_VERSION")
+
+
+def test_workspace_queries(lib):
+    f1 = _lib.forward_workspace_bytes(1024, 896, 151936, _lib.CCE_REDUCTION_MEAN)
+    f2 = _lib.forward_workspace_bytes(2048, 896, 151936, _lib.CCE_REDUCTION_MEAN)
+    assert 0 < f1 < f2
+    # forward scratch is O(N): the row partials, never N x V
+    assert f2 < 2048 * 151936
+    b = _lib.backward_workspace_bytes(16384, 896, 151936, 8192, True, True)
+    # at least one band of G (N x chunk bf16), far below N x V
+    assert 16384 * 8192 * 2 <= b < 16384 * 151936 * 2
+    b_frozen = _lib.backward_workspace_bytes(16384, 896, 151936, 8192, True, False)
+    assert b_frozen < b
+    # empty batch is a valid problem
+    assert _lib.forward_workspace_bytes(0, 64, 300, _lib.CCE_REDUCTION_MEAN) > 0
+    assert _lib.forward_workspace_bytes(0, 64, 300, _lib.CCE_REDUCTION_NONE) > 0
+    assert _lib.backward_workspace_bytes(0, 64, 300, 8192, True, True) >= 0
+    # chunk_size bounds the band
+    assert _lib.backward_workspace_bytes(16384, 896, 151936, 2048, True, True) < b
+
+
+@pytest.mark.parametrize("N,d,V,red,msg", [
+    (16, 7, 100, 1, "multiple of 8"),
+    (16, 0, 100, 1, "multiple of 8"),
+    (16, 64, 0, 1, "vocab"),
+    (-1, 64, 10, 1, "N must be"),
+    (16, 64, 100, 5, "reduction"),
+])
+def test_workspace_query_rejects_bad_arguments(lib, N, d, V, red, msg):
+    out = ctypes.c_size_t(0)
+    rc = lib.cce_forward_workspace_bytes(N, d, V, red, ctypes.byref(out))
+    assert rc == _lib.CCE_ERR_INVALID_ARG
+    assert msg in lib.cce_last_error().decode()
+
+
+def test_forward_rejects_small_workspace_before_launch(lib):
+    fake = 0x10000  # never dereferenced: validation fails first
+    rc = lib.cce_forward(fake, fake, fake, 1, None, 64, 64, 1000, -100, 0.0, 0.0, _lib.CCE_REDUCTION_MEAN,
+                         fake, fake, fake, fake, 16, None)
+    assert rc == _lib.CCE_ERR_WORKSPACE
+    assert "workspace too small" in lib.cce_last_error().decode()
+
+
+def test_forward_rejects_null_inputs(lib):
+    rc = lib.cce_forward(None, None, None, 1, None, 64, 64, 1000, -100, 0.0, 0.0, _lib.CCE_REDUCTION_MEAN,
+                         0x10000, 0x10000, 0x10000, 0x10000, 1 << 20, None)
+    assert rc == _lib.CCE_ERR_INVALID_ARG
+
+
+def test_backward_rejects_bad_dtype_and_bias(lib):
+    fake = 0x10000
+    rc = lib.cce_backward(fake, fake, fake, fake, 1, None, fake, fake, 64, 64, 1000, -100, 0.0, 0.0, 1, 8192,
+                          fake, 7, None, 0, None, fake, 1 << 30, None)
+    assert rc == _lib.CCE_ERR_INVALID_ARG and "dtype" in lib.cce_last_error().decode()
+    rc = lib.cce_backward(fake, fake, fake, fake, 1, None, fake, fake, 64, 64, 1000, -100, 0.0, 0.0, 1, 8192,
+                          fake, 0, None, 0, fake, fake, 1 << 30, None)
+    assert rc == _lib.CCE_ERR_INVALID_ARG and "bias" in lib.cce_last_error().decode()
+
+
+def test_misaligned_pointers_rejected(lib):
+    rc = lib.cce_forward(0x10002, 0x10000, 0x10000, 1, None, 64, 64, 1000, -100, 0.0, 0.0, 1,
+                         0x10000, 0x10000, 0x10000, 0x10000, 1 << 20, None)
+    assert rc == _lib.CCE_ERR_INVALID_ARG and "aligned" in lib.cce_last_error().decode()
+
+
+def test_build_command_targets_gfx950():
+    cmd = _build.compile_command("/tmp/x.so")
+    assert "--offload-arch=gfx950" in cmd
+    assert "-packed-fp32-ops" in cmd

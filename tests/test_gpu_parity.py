@@ -1,0 +1,209 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle.
+
+Inputs are rounded to bf16 before either side sees them (the kernels compute
+in bf16 with fp32 accumulation), so the comparison measures the kernels'
+own error.  Tolerances (tests/cce_common.py): loss within 1e-3 relative;
+gradients with max abs error <= 2e-2 * max|ref| and cosine >= 0.9999.
+Full-size configurations use a materialised fp32 torch reference on the GPU.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import cce_oracle as oracle
+from tests.cce_common import (CONFIGS, IGNORE, assert_grad_close, assert_loss_close, bf16_exact, grad_report,
+                              make_inputs, torch_reference)
+
+pytestmark = pytest.mark.gpu
+
+
+def _cce():
+    from chronicals_amd.kernels.cut_cross_entropy import cut_cross_entropy
+    return cut_cross_entropy
+
+
+def run_hip(dev, h, w, lab, b=None, chunk=8192, eps=0.0, z=0.0, reduction="mean", grad_output=None,
+            need_dh=True, need_dw=True, need_db=True, hdtype=torch.bfloat16, wdtype=torch.bfloat16):
+    hd = h.detach().to(dev, hdtype).requires_grad_(need_dh)
+    wd = w.detach().to(dev, wdtype).requires_grad_(need_dw)
+    bd = None if b is None else b.detach().to(dev, torch.float32).requires_grad_(need_db)
+    ld = lab.to(dev)
+    loss = _cce()(hd, wd, ld, bd, chunk, IGNORE, eps, z, reduction=reduction)
+    if need_dh or need_dw or (b is not None and need_db):
+        if reduction == "none":
+            go = torch.ones_like(loss) if grad_output is None else grad_output.to(dev).reshape(loss.shape)
+            loss.backward(go)
+        else:
+            loss.backward(None if grad_output is None else torch.tensor(float(grad_output), device=dev))
+    torch.cuda.synchronize()
+    out = {"loss": loss.detach().float().cpu().numpy()}
+    out["dh"] = None if not need_dh else hd.grad.float().cpu().numpy()
+    out["dw"] = None if not need_dw else wd.grad.float().cpu().numpy()
+    out["db"] = None if (b is None or not need_db) else bd.grad.float().cpu().numpy()
+    return out
+
+
+def run_oracle(h, w, lab, b=None, chunk=8192, eps=0.0, z=0.0, reduction="mean", grad_output=None):
+    hn = bf16_exact(h).numpy().reshape(-1, h.shape[-1])
+    wn = bf16_exact(w).numpy()
+    bn = None if b is None else b.float().numpy()
+    go = None
+    if grad_output is not None:
+        go = np.asarray(grad_output.numpy() if torch.is_tensor(grad_output) else [grad_output], np.float64)
+    loss, lse, gh, gw, gb = oracle.loss_and_grads(hn, wn, lab.numpy().reshape(-1), bn, chunk_size=chunk,
+                                                  label_smoothing=eps, z_loss_weight=z, reduction=reduction,
+                                                  grad_output=go)
+    return {"loss": np.asarray(loss).reshape(np.asarray(lab).shape) if reduction == "none" else loss,
+            "lse": lse, "dh": gh, "dw": gw, "db": gb}
+
+
+def compare(got, ref, tag):
+    assert_loss_close(got["loss"], ref["loss"], f"{tag} loss")
+    for k in ("dh", "dw", "db"):
+        if got.get(k) is not None and ref.get(k) is not None:
+            assert_grad_close(got[k].reshape(ref[k].shape), ref[k], f"{tag} {k}")
+
+
+def _rand_case(N, d, V, seed=0, ignore_frac=0.1, bias=False, wscale=0.05):
+    g = torch.Generator().manual_seed(seed)
+    h = torch.randn(N, d, generator=g)
+    w = torch.randn(V, d, generator=g) * wscale
+    lab = torch.randint(0, V, (N,), generator=g)
+    if N:
+        lab[torch.rand(N, generator=g) < ignore_frac] = IGNORE
+    b = torch.randn(V, generator=g) * 0.1 if bias else None
+    return h, w, lab, b
+
+
+@pytest.mark.parametrize("N,d,V,chunk", [
+    (256, 64, 256, 8192),      # one tile
+    (1, 8, 1, 8192),           # smallest problem
+    (3, 16, 7, 8192),
+    (255, 72, 257, 256),       # ragged rows / columns, two bands
+    (257, 136, 1000, 512),     # d not a multiple of 64, ragged bands
+    (600, 128, 5000, 1024),
+    (513, 264, 3001, 8192),
+])
+def test_ragged_shapes(gpu, N, d, V, chunk):
+    print(f"case N={N} d={d} V={V} chunk={chunk}", flush=True)
+    h, w, lab, _ = _rand_case(N, d, V, seed=N + V)
+    compare(run_hip(gpu, h, w, lab, chunk=chunk), run_oracle(h, w, lab, chunk=chunk), f"N{N}d{d}V{V}")
+
+
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+@pytest.mark.parametrize("bias", [False, True])
+def test_reductions_and_bias(gpu, reduction, bias):
+    print(f"case reduction={reduction} bias={bias}", flush=True)
+    h, w, lab, b = _rand_case(300, 96, 2000, seed=11, bias=bias)
+    go = torch.rand(300, generator=torch.Generator().manual_seed(3)) if reduction == "none" else 0.7
+    got = run_hip(gpu, h, w, lab, b, chunk=768, reduction=reduction, grad_output=go)
+    ref = run_oracle(h, w, lab, b, chunk=768, reduction=reduction, grad_output=go)
+    compare(got, ref, f"{reduction}/bias={bias}")
+
+
+@pytest.mark.parametrize("eps,z", [(0.1, 0.0), (0.0, 1e-3), (0.1, 1e-4)])
+def test_label_smoothing_and_zloss(gpu, eps, z):
+    print(f"case eps={eps} z={z}", flush=True)
+    h, w, lab, b = _rand_case(400, 64, 3000, seed=5, bias=True)
+    compare(run_hip(gpu, h, w, lab, b, chunk=1024, eps=eps, z=z),
+            run_oracle(h, w, lab, b, chunk=1024, eps=eps, z=z), f"eps{eps}z{z}")
+
+
+def test_out_of_range_labels(gpu):
+    h, w, lab, _ = _rand_case(64, 32, 500, seed=2)
+    lab[3] = 500
+    lab[4] = 10**6
+    lab[5] = -5
+    compare(run_hip(gpu, h, w, lab), run_oracle(h, w, lab), "oob")
+
+
+def test_all_ignored(gpu):
+    h, w, lab, b = _rand_case(100, 64, 700, seed=9, bias=True)
+    lab[:] = IGNORE
+    got = run_hip(gpu, h, w, lab, b)
+    assert float(got["loss"]) == 0.0
+    assert not np.any(got["dh"]) and not np.any(got["dw"]) and not np.any(got["db"])
+
+
+def test_empty_batch(gpu):
+    h = torch.zeros(0, 64)
+    w = torch.randn(300, 64) * 0.02
+    lab = torch.zeros(0, dtype=torch.int64)
+    got = run_hip(gpu, h, w, lab)
+    assert float(got["loss"]) == 0.0
+    assert got["dw"].shape == (300, 64) and not np.any(got["dw"])
+
+
+def test_frozen_weight_and_int32_labels_and_3d(gpu):
+    h, w, lab, _ = _rand_case(2 * 150, 80, 1500, seed=21)
+    h3 = h.reshape(2, 150, 80)
+    lab3 = lab.reshape(2, 150).to(torch.int32)
+    got = run_hip(gpu, h3, w, lab3, need_dw=False)
+    ref = run_oracle(h, w, lab)
+    assert got["dw"] is None
+    assert_loss_close(got["loss"], ref["loss"])
+    assert_grad_close(got["dh"].reshape(ref["dh"].shape), ref["dh"], "dh (frozen W)")
+
+
+def test_fp32_and_fp16_inputs_return_input_dtypes(gpu):
+    h, w, lab, _ = _rand_case(128, 64, 900, seed=4)
+    from chronicals_amd.kernels.cut_cross_entropy import cut_cross_entropy
+    for dt in (torch.float32, torch.float16):
+        hd = h.to(gpu, dt).requires_grad_(True)
+        wd = w.to(gpu, dt).requires_grad_(True)
+        loss = cut_cross_entropy(hd, wd, lab.to(gpu))
+        loss.backward()
+        assert loss.dtype == torch.float32 and hd.grad.dtype == dt and wd.grad.dtype == dt
+        ref = run_oracle(h, w, lab)
+        assert_loss_close(loss.item(), ref["loss"])
+        assert_grad_close(hd.grad.float().cpu().numpy(), ref["dh"], f"dh {dt}")
+        assert_grad_close(wd.grad.float().cpu().numpy(), ref["dw"], f"dw {dt}")
+
+
+def test_c1_full_vs_oracle(gpu):
+    """C1 (N=256, d=768, V=50257, fp32 inputs, 10% ignored) at full size."""
+    cfg = CONFIGS["C1"]
+    h, w, lab = make_inputs(cfg, seed=0)
+    print("case C1 full", flush=True)
+    got = run_hip(gpu, h, w, lab, chunk=8192, hdtype=torch.float32, wdtype=torch.float32)
+    ref = run_oracle(h, w, lab, chunk=8192)
+    compare(got, ref, "C1")
+    # against the unrounded fp32 inputs too: the bf16 rounding at the boundary stays inside the contract
+    raw = oracle.loss_and_grads(h.numpy(), w.numpy(), lab.numpy(), chunk_size=8192)
+    assert_loss_close(got["loss"], raw[0], "C1 loss vs fp32 oracle")
+    assert_grad_close(got["dh"], raw[2], "C1 dh vs fp32 oracle")
+    assert_grad_close(got["dw"], raw[3], "C1 dw vs fp32 oracle")
+
+
+@pytest.mark.parametrize("name,n", [("C2", 512), ("C3", 256), ("C4", 512), ("C5", 256)])
+def test_config_row_slice_vs_oracle(gpu, name, n):
+    """Full d and V of each configuration on a slice of rows (the oracle's cost is linear in N)."""
+    cfg = CONFIGS[name]
+    print(f"case {name} rows={n}", flush=True)
+    h, w, lab = make_inputs(cfg, seed=0, N=n)
+    got = run_hip(gpu, h, w, lab)
+    ref = run_oracle(h, w, lab)
+    compare(got, ref, f"{name}[:{n}]")
+
+
+def test_deterministic(gpu):
+    h, w, lab, b = _rand_case(700, 128, 4000, seed=8, bias=True)
+    a = run_hip(gpu, h, w, lab, b, chunk=1024)
+    c = run_hip(gpu, h, w, lab, b, chunk=1024)
+    for k in ("loss", "dh", "dw", "db"):
+        assert np.array_equal(a[k], c[k]), k
+
+
+@pytest.mark.parametrize("name", ["C2"])
+def test_full_size_vs_torch_fp32(gpu, name):
+    """Full configuration against a materialised-logits fp32 torch reference on the GPU."""
+    cfg = CONFIGS[name]
+    print(f"case {name} full vs torch fp32", flush=True)
+    h, w, lab = make_inputs(cfg, seed=0, device=gpu, gen_device="cuda")
+    got = run_hip(gpu, h, w, lab)
+    ref = torch_reference(bf16_exact(h), bf16_exact(w), lab, dtype=torch.float32)
+    rep = {k: grad_report(got[k], ref[k].cpu().numpy()) for k in ("dh", "dw")}
+    print(f"{name} loss {float(got['loss']):.6f} ref {float(ref['loss']):.6f} {rep}", flush=True)
+    assert_loss_close(got["loss"], ref["loss"].cpu().numpy(), f"{name} loss")
+    assert_grad_close(got["dh"], ref["dh"].cpu().numpy(), f"{name} dh")
+    assert_grad_close(got["dw"], ref["dw"].cpu().numpy(), f"{name} dw")

@@ -1,0 +1,85 @@
+"""Host-side API of chronicals_amd.kernels.cut_cross_entropy (no GPU needed).
+
+Mirrors the reference module's helpers (chronicals/kernels/cut_cross_entropy.py):
+get_optimal_chunk_size :59-90, estimate_memory_savings :1403-1430,
+CutCrossEntropyLoss :1081-1162, and checks that the product path refuses CPU
+tensors instead of falling back to a CPU implementation.
+"""
+import inspect
+
+import pytest
+import torch
+
+from chronicals_amd.kernels import cut_cross_entropy as cce
+
+
+@pytest.mark.parametrize("V,d,gb,expect", [
+    (50257, 768, 40.0, 4096),
+    (100000, 4096, 40.0, 8192),
+    (151936, 896, 40.0, 16384),
+    (128256, 4096, 40.0, 16384),
+    (151936, 896, 0.001, 256),          # VRAM cap, floor 256
+    (151936, 8192, 0.5, 4096),          # 0.5*0.8 GiB / (8*8192 B) = 6553 -> 4096
+])
+def test_get_optimal_chunk_size(V, d, gb, expect):
+    assert cce.get_optimal_chunk_size(V, d, gb) == expect
+
+
+def test_estimate_memory_savings():
+    r = cce.estimate_memory_savings(1, 8192, 151936, 8192)
+    assert r["standard_mb"] == pytest.approx(8192 * 151936 * 8 / 2 ** 20)
+    assert r["cce_mb"] == pytest.approx(8192 * 8192 * 8 / 2 ** 20)
+    assert r["reduction_factor"] == pytest.approx(151936 / 8192)
+    assert r["savings_mb"] == pytest.approx(r["standard_mb"] - r["cce_mb"])
+
+
+def test_signature_matches_reference_order():
+    params = list(inspect.signature(cce.cut_cross_entropy).parameters)
+    assert params[:9] == ["hidden", "weight", "labels", "bias", "chunk_size", "ignore_index", "label_smoothing",
+                          "z_loss_weight", "use_triton"]
+    assert "reduction" in params
+    sig = inspect.signature(cce.cut_cross_entropy)
+    assert sig.parameters["chunk_size"].default == 8192
+    assert sig.parameters["ignore_index"].default == -100
+    assert sig.parameters["reduction"].default == "mean"
+
+
+def test_loss_module_accepts_all_reductions_and_rejects_others():
+    for red in ("mean", "sum", "none"):
+        m = cce.CutCrossEntropyLoss(reduction=red)
+        assert m.reduction == red
+    with pytest.raises(ValueError):
+        cce.CutCrossEntropyLoss(reduction="avg")
+    m = cce.CutCrossEntropyLoss(chunk_size=4096, z_loss_weight=1e-4)
+    assert m.extra_repr() == "chunk_size=4096, ignore_index=-100, label_smoothing=0.0, z_loss_weight=0.0001"
+
+
+def test_reference_constants():
+    assert (cce.CHUNK_SIZE_SMALL_VOCAB, cce.CHUNK_SIZE_MEDIUM_VOCAB, cce.CHUNK_SIZE_LARGE_VOCAB) == (4096, 8192, 16384)
+    assert cce.DEFAULT_VOCAB_CHUNK_SIZE == 8192
+    assert cce.TRITON_BLOCK_SIZE_MAX == 32768
+
+
+def test_cpu_tensors_are_refused_not_computed():
+    h = torch.randn(4, 8)
+    w = torch.randn(10, 8)
+    lab = torch.zeros(4, dtype=torch.long)
+    with pytest.raises(RuntimeError, match="HIP devices"):
+        cce.cut_cross_entropy(h, w, lab)
+    with pytest.raises(RuntimeError, match="HIP devices"):
+        cce.CutCrossEntropyLoss()(h, w, lab)
+
+
+def test_bad_reduction_rejected_before_compute():
+    with pytest.raises(ValueError):
+        cce.cut_cross_entropy(torch.randn(2, 8), torch.randn(3, 8), torch.zeros(2, dtype=torch.long),
+                              reduction="max")
+
+
+def test_package_does_not_import_oracle():
+    import pathlib
+    root = pathlib.Path(cce.__file__).resolve().parents[1]
+    for py in root.rglob("*.py"):
+        text = py.read_text()
+        for pat in ("import oracle", "from oracle", "cce_oracle"):
+            assert pat not in text, f"{py} reaches the oracle ({pat})"
