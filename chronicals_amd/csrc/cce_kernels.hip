@@ -35,6 +35,8 @@
 #include <math.h>
 #include <float.h>
 
+#include <type_traits>
+
 #include "../../include/chronicals_cce.h"
 
 namespace {
@@ -44,8 +46,32 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kThreads = 512;         // 8 waves of 64
+// Per-GEMM configuration (wave layout W, column tile BN, pipeline PIPE);
+// overridable at build time for tuning.
+#ifndef CCE_W_LSE
+#define CCE_W_LSE 8
+#endif
+#ifndef CCE_W_GRAD
+#define CCE_W_GRAD 8
+#endif
+#ifndef CCE_W_ACC
+#define CCE_W_ACC 8
+#endif
+#ifndef CCE_BN_LSE
+#define CCE_BN_LSE 128
+#endif
+#ifndef CCE_BN_GRAD
+#define CCE_BN_GRAD 256
+#endif
+#ifndef CCE_PIPE_GRAD
+#define CCE_PIPE_GRAD 1
+#endif
+#ifndef CCE_PIPE_LSE
+#define CCE_PIPE_LSE 3
+#endif
+
 constexpr int kBM = 256;              // rows of a workgroup tile
 constexpr int kBK = 64;               // K slab per pipeline step
 constexpr int kPitch = kBK + 8;       // LDS row pitch in bf16 (144 B: conflict-free b128 reads)
@@ -55,8 +81,10 @@ constexpr float kNegBig = -FLT_MAX;   // finite "minus infinity" for running max
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ inline f32x4 mfma_16x16x32(u32x4 a, u32x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+// v_mfma_f32_32x32x16_bf16 (on gfx950 it issues at about twice the rate of
+// the 16x16x32 form, measured: ~2.2 vs ~0.8-1.2 PFLOP/s device-wide).
+__device__ inline f32x16 mfma_32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
@@ -92,28 +120,48 @@ __device__ inline void grouped_map(int bid, int nb, int gm, int gn, int& pm, int
 // (k contiguous, pitch kPitch) so one MFMA fragment read serves both layouts.
 // ---------------------------------------------------------------------------
 
+// 16 zero bytes in device memory: out-of-range lanes load from here.
+__device__ __attribute__((aligned(16))) uint32_t g_zero16[4];
+
+// 16-byte load that is issued unconditionally: out-of-range lanes read the
+// zero block instead, so the value needs no select after the load.  Keeping
+// the load out of divergent control flow and unconsumed until its LDS store
+// lets the compiler count outstanding loads exactly instead of draining them.
+__device__ inline u32x4 guarded_load(const bf16_t* __restrict__ X, long off, bool ok) {
+  const u32x4* p = ok ? reinterpret_cast<const u32x4*>(X + off) : reinterpret_cast<const u32x4*>(g_zero16);
+  return *p;
+}
+
+// Per-kernel wave layout.  W = 8: two waves per SIMD, 64-row wave tiles,
+// accumulators in VGPRs.  W = 4: one wave per SIMD, 128-row wave tiles,
+// accumulators in AGPRs.  Waves form (256 / kWaveRows) x 2 over a tile.
+template <int W>
+struct WaveCfg {
+  static constexpr int kThreads = W * 64;
+  static constexpr int kWaveRows = (W == 8) ? 64 : 128;
+  static constexpr int kFM = kWaveRows / 32;  // 32-row MFMA blocks per wave tile
+};
+
 // K-major operand: element (r, k) at X[r*ld + k].
-template <int BR>
+template <int BR, int W>
 struct LoadKMajor {
-  static constexpr int kN = BR * (kBK / 8) / kThreads;  // 16-byte chunks per thread
+  static constexpr int kT = W * 64;
+  static constexpr int kN = BR * (kBK / 8) / kT;  // 16-byte chunks per thread
   u32x4 v[kN];
   __device__ inline void load(const bf16_t* __restrict__ X, long ld, int r0, int rlim, int k0, int K,
                               int tid) {
 #pragma unroll
     for (int i = 0; i < kN; ++i) {
-      const int c = tid + i * kThreads;
+      const int c = tid + i * kT;
       const int row = c >> 3, kc = (c & 7) * 8;
       const int gr = r0 + row, gk = k0 + kc;
-      if (gr < rlim && gk < K)
-        v[i] = *reinterpret_cast<const u32x4*>(X + (long)gr * ld + gk);
-      else
-        v[i] = u32x4{0u, 0u, 0u, 0u};
+      v[i] = guarded_load(X, (long)gr * ld + gk, gr < rlim && gk < K);
     }
   }
   __device__ inline void store(bf16_t* S, int tid) const {
 #pragma unroll
     for (int i = 0; i < kN; ++i) {
-      const int c = tid + i * kThreads;
+      const int c = tid + i * kT;
       const int row = c >> 3, kc = (c & 7) * 8;
       *reinterpret_cast<u32x4*>(S + row * kPitch + kc) = v[i];
     }
@@ -121,46 +169,53 @@ struct LoadKMajor {
 };
 
 // MN-major operand (256-row tiles): element (r, k) at X[k*ld + r].  Each
-// thread loads a 4(k) x 8(r) block with four 16-byte loads, transposes it in
-// registers and writes eight 8-byte [r][k] pieces to LDS.  Lanes 0..15 of a
-// wave walk k, so the 8-byte LDS writes of 16 lanes cover 32 distinct banks.
+// thread loads 4(k) x 8(r) blocks with 16-byte loads, transposes them in
+// registers and writes 8-byte [r][k] pieces to LDS.  Lanes 0..15 of a wave
+// walk k, so the 8-byte LDS writes of 16 lanes cover 32 distinct banks.
+template <int W>
 struct LoadMNMajor256 {
-  u32x4 v[4];
+  static constexpr int kB = 512 / (W * 64);  // 4x8 blocks per thread
+  u32x4 v[kB][4];
   __device__ inline void load(const bf16_t* __restrict__ X, long ld, int r0, int rlim, int k0, int K,
                               int tid) {
     const int w = tid >> 6, l = tid & 63;
-    const int kq = l & 15, rb = (w << 2) + (l >> 4);
-    const int gr = r0 + rb * 8;
+    const int kq = l & 15;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int gk = k0 + kq * 4 + i;
-      if (gk < K && gr < rlim)
-        v[i] = *reinterpret_cast<const u32x4*>(X + (long)gk * ld + gr);
-      else
-        v[i] = u32x4{0u, 0u, 0u, 0u};
+    for (int t = 0; t < kB; ++t) {
+      const int rb = (w * kB + t) * 4 + (l >> 4);
+      const int gr = r0 + rb * 8;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int gk = k0 + kq * 4 + i;
+        v[t][i] = guarded_load(X, (long)gk * ld + gr, gk < K && gr < rlim);
+      }
     }
   }
   __device__ inline void store(bf16_t* S, int tid) const {
     const int w = tid >> 6, l = tid & 63;
-    const int kq = l & 15, rb = (w << 2) + (l >> 4);
+    const int kq = l & 15;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t a0 = v[0][q], a1 = v[1][q], a2 = v[2][q], a3 = v[3][q];
-      const u32x2 ev = {(a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16)};
-      const u32x2 od = {(a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u)};
-      *reinterpret_cast<u32x2*>(S + (rb * 8 + 2 * q) * kPitch + kq * 4) = ev;
-      *reinterpret_cast<u32x2*>(S + (rb * 8 + 2 * q + 1) * kPitch + kq * 4) = od;
+    for (int t = 0; t < kB; ++t) {
+      const int rb = (w * kB + t) * 4 + (l >> 4);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t a0 = v[t][0][q], a1 = v[t][1][q], a2 = v[t][2][q], a3 = v[t][3][q];
+        const u32x2 ev = {(a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16)};
+        const u32x2 od = {(a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u)};
+        *reinterpret_cast<u32x2*>(S + (rb * 8 + 2 * q) * kPitch + kq * 4) = ev;
+        *reinterpret_cast<u32x2*>(S + (rb * 8 + 2 * q + 1) * kPitch + kq * 4) = od;
+      }
     }
   }
 };
 
-template <bool KMAJ, int BR>
+template <bool KMAJ, int BR, int W>
 struct LoaderSel {
-  typedef LoadKMajor<BR> type;
+  typedef LoadKMajor<BR, W> type;
 };
-template <>
-struct LoaderSel<false, 256> {
-  typedef LoadMNMajor256 type;
+template <int W>
+struct LoaderSel<false, 256, W> {
+  typedef LoadMNMajor256<W> type;
 };
 
 struct GemmShape {
@@ -171,49 +226,92 @@ struct GemmShape {
   int M, N, K;
 };
 
-// One BK=64 slab of MFMA work for a wave: wave tile 64 x (BN/2), 16x16x32
-// instructions.  The B fragment is passed as the instruction's first operand,
-// so the accumulator holds C^T in the hardware's 16x16 layout: lane l owns
-// C[m = i*16 + (l & 15)][n = j*16 + (l >> 4)*4 + r], r = 0..3 (four
-// consecutive columns of one row).
-template <int BN>
-__device__ inline void mma_slab(const bf16_t* __restrict__ As, const bf16_t* __restrict__ Bs,
-                                f32x4 (&acc)[4][BN / 32], int wm, int wn, int l) {
-  constexpr int FN = BN / 32;
+// Accumulator tile of one wave: kWaveRows rows x (BN/2) columns as
+// kFM x (BN/64) blocks of 32x32 fp32.
+template <int BN, int W>
+struct WaveAcc {
+  static constexpr int FM = WaveCfg<W>::kFM;
+  static constexpr int FN = BN / 64;
+  f32x16 v[FM][FN];
+  __device__ inline void zero() {
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    const int kof = kk * 32 + (l >> 4) * 8;
-    u32x4 a[4], b[FN];
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      a[i] = *reinterpret_cast<const u32x4*>(As + (wm * 64 + i * 16 + (l & 15)) * kPitch + kof);
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
-      b[j] = *reinterpret_cast<const u32x4*>(Bs + (wn * (BN / 2) + j * 16 + (l & 15)) * kPitch + kof);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = mfma_16x16x32(b[j], a[i], acc[i][j]);
+        for (int r = 0; r < 16; ++r) v[i][j][r] = 0.f;
   }
+};
+
+// Lane <-> element map of a wave tile.  The B fragment is passed as the
+// instruction's first operand, so each 32x32 block holds C^T in the hardware
+// layout: lane l owns row m = i*32 + (l & 31) and, for register r = 4q + e,
+// column n = j*32 + 8q + 4*(l >> 5) + e — four consecutive columns per q.
+template <int W>
+__device__ inline int acc_row(int wm, int i, int l) {
+  return wm * WaveCfg<W>::kWaveRows + i * 32 + (l & 31);
+}
+template <int BN>
+__device__ inline int acc_col(int wn, int j, int q, int l) {
+  return wn * (BN / 2) + j * 32 + q * 8 + (l >> 5) * 4;
+}
+
+// Opaque copies of the lane id and tile coordinates: epilogue address and
+// mask arithmetic then cannot be hoisted above the K loop, where it would
+// stay live next to the accumulators.
+__device__ inline void pin_epilogue(int& l, int& tm, int& tn) {
+  asm volatile("" : "+v"(l));
+  asm volatile("" : "+s"(tm), "+s"(tn));
+}
+
+// Register fragments of one k-step (16 of K) for a wave.
+template <int BN, int W>
+struct Frags {
+  u32x4 a[WaveCfg<W>::kFM], b[BN / 64];
+};
+
+template <int BN, int W>
+__device__ inline void read_frags(const bf16_t* __restrict__ As, const bf16_t* __restrict__ Bs, int kk,
+                                  Frags<BN, W>& f, int wm, int wn, int l) {
+  const int kof = kk * 16 + (l >> 5) * 8;
+#pragma unroll
+  for (int i = 0; i < WaveCfg<W>::kFM; ++i)
+    f.a[i] = *reinterpret_cast<const u32x4*>(As + (wm * WaveCfg<W>::kWaveRows + i * 32 + (l & 31)) * kPitch + kof);
+#pragma unroll
+  for (int j = 0; j < BN / 64; ++j)
+    f.b[j] = *reinterpret_cast<const u32x4*>(Bs + (wn * (BN / 2) + j * 32 + (l & 31)) * kPitch + kof);
+}
+
+// v_mfma_f32_32x32x16_bf16 over the kFM x (BN/64) blocks of one k-step.
+template <int BN, int W>
+__device__ inline void mfma_frags(const Frags<BN, W>& f, WaveAcc<BN, W>& acc) {
+#pragma unroll
+  for (int i = 0; i < WaveCfg<W>::kFM; ++i)
+#pragma unroll
+    for (int j = 0; j < BN / 64; ++j) acc.v[i][j] = mfma_32x32x16(f.b[j], f.a[i], acc.v[i][j]);
 }
 
 // ---------------------------------------------------------------------------
 // Epilogues
 // ---------------------------------------------------------------------------
 
+struct LseParams {
+  const float* bias;  // [V] or null
+  float* pm;          // [splits][M] running max (log2 units)
+  float* ps;          // [splits][M] sum of 2^(x - max)
+  int splits;
+  int tiles_n;
+};
+
 // Forward: per-row online (max, sum-exp) in base 2 over the workgroup's run of
 // vocabulary tiles; at the end one partial per (row, split) is written.
-template <int BN>
-struct EpiLse {
-  struct Params {
-    const float* bias;  // [V] or null
-    float* pm;          // [splits][M] running max (log2 units)
-    float* ps;          // [splits][M] sum of 2^(x - max)
-    int splits;
-    int tiles_n;
-  };
+template <int BN, int W, bool HB>
+struct EpiLseT {
+  typedef LseParams Params;
+  static constexpr bool kMultiTile = true;
+  static constexpr int FM = WaveCfg<W>::kFM;
   struct State {
-    float m[4], s[4];
+    float m[FM], s[FM];
   };
   static __device__ inline void assign(const GemmShape& g, const Params& p, int bid, int nb, int& tm,
                                        int& t0, int& t1, int& split) {
@@ -226,40 +324,65 @@ struct EpiLse {
   }
   static __device__ inline void init(State& st) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < FM; ++i) {
       st.m[i] = kNegBig;
       st.s[i] = 0.f;
     }
   }
-  static __device__ inline void tile(const Params& p, State& st, f32x4 (&acc)[4][BN / 32],
-                                     const GemmShape& g, int tm, int tn, int wm, int wn, int l) {
-    constexpr int FN = BN / 32;
-    float add[FN * 4];
+  static __device__ inline void tile(const Params& p, State& st, WaveAcc<BN, W>& acc, const GemmShape& g, int tm,
+                                     int tn, int wm, int wn, int l) {
+    constexpr int FN = BN / 64;
+    pin_epilogue(l, tm, tn);
+    const int c0 = tn * BN;
+    if (!HB && c0 + BN <= g.N) {
+      // interior tile: max over raw logits (log2e > 0 commutes with max), then
+      // one fused exp2(x*log2e - m) per element
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+      for (int i = 0; i < FM; ++i) {
+        float mx = kNegBig;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int col = tn * BN + wn * (BN / 2) + j * 16 + (l >> 4) * 4 + r;
-        add[j * 4 + r] = (col < g.N) ? (p.bias ? p.bias[col] : 0.f) : -INFINITY;
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, acc.v[i][j][r]);
+        const float mn = fmaxf(st.m[i], mx * kLog2e);
+        float sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sum += fast_exp2(__builtin_fmaf(acc.v[i][j][r], kLog2e, -mn));
+        st.s[i] = st.s[i] * fast_exp2(st.m[i] - mn) + sum;
+        st.m[i] = mn;
+        __builtin_amdgcn_sched_barrier(0);
       }
+      return;
+    }
+    // edge tile or bias: per-column offset, columns past V excluded
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float x[FN * 4];
+    for (int i = 0; i < FM; ++i) {
       float mx = kNegBig;
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float v = (acc[i][j][r] + add[j * 4 + r]) * kLog2e;
-          x[j * 4 + r] = v;
-          mx = fmaxf(mx, v);
-        }
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int col = c0 + acc_col<BN>(wn, j, q, l) + e;
+            if (col < g.N) mx = fmaxf(mx, (acc.v[i][j][4 * q + e] + (HB ? p.bias[col] : 0.f)) * kLog2e);
+          }
       const float mn = fmaxf(st.m[i], mx);
       float sum = 0.f;
 #pragma unroll
-      for (int q = 0; q < FN * 4; ++q) sum += fast_exp2(x[q] - mn);
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int col = c0 + acc_col<BN>(wn, j, q, l) + e;
+            if (col < g.N) sum += fast_exp2((acc.v[i][j][4 * q + e] + (HB ? p.bias[col] : 0.f)) * kLog2e - mn);
+          }
       st.s[i] = st.s[i] * fast_exp2(st.m[i] - mn) + sum;
       st.m[i] = mn;
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   static __device__ inline void merge(float& m, float& s, float m2, float s2) {
@@ -269,25 +392,23 @@ struct EpiLse {
   }
   static __device__ inline void finish(const Params& p, State& st, const GemmShape& g, int tm, int split,
                                        bf16_t* smem, int wm, int wn, int l) {
+    // lanes l and l+32 hold the same rows
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      merge(st.m[i], st.s[i], __shfl_xor(st.m[i], 16), __shfl_xor(st.s[i], 16));
-      merge(st.m[i], st.s[i], __shfl_xor(st.m[i], 32), __shfl_xor(st.s[i], 32));
-    }
+    for (int i = 0; i < FM; ++i) merge(st.m[i], st.s[i], __shfl_xor(st.m[i], 32), __shfl_xor(st.s[i], 32));
     float* red = reinterpret_cast<float*>(smem);
-    if (wn == 1 && l < 16) {
+    if (wn == 1 && l < 32) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = wm * 64 + i * 16 + l;
+      for (int i = 0; i < FM; ++i) {
+        const int row = acc_row<W>(wm, i, l);
         red[row] = st.m[i];
         red[kBM + row] = st.s[i];
       }
     }
     __syncthreads();
-    if (wn == 0 && l < 16) {
+    if (wn == 0 && l < 32) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = wm * 64 + i * 16 + l;
+      for (int i = 0; i < FM; ++i) {
+        const int row = acc_row<W>(wm, i, l);
         merge(st.m[i], st.s[i], red[row], red[kBM + row]);
         const int grow = tm * kBM + row;
         if (grow < g.M) {
@@ -299,18 +420,27 @@ struct EpiLse {
   }
 };
 
+template <int BN, int W>
+using EpiLse = EpiLseT<BN, W, false>;
+template <int BN, int W>
+using EpiLseBias = EpiLseT<BN, W, true>;
+
+struct GradParams {
+  const float* bias;     // [V] or null (full vocabulary, indexed by v0 + c)
+  const float4* rowp;    // [M]
+  const int* rowlab;     // [M] target column or -1
+  bf16_t* G;             // [M][ldg]
+  long ldg;
+  int v0;                // first vocabulary row of the band
+};
+
 // Backward recompute: G[n][c] = dLoss/dS for one vocabulary band, stored bf16.
 // rowp[n] = {lse*log2e, cP, cT, cU}: g = cP*2^(x*log2e - lse2) - cU - cT*[c == label].
-template <int BN>
-struct EpiGrad {
-  struct Params {
-    const float* bias;     // [V] or null (full vocabulary, indexed by v0 + c)
-    const float4* rowp;    // [M]
-    const int* rowlab;     // [M] target column or -1
-    bf16_t* G;             // [M][ldg]
-    long ldg;
-    int v0;                // first vocabulary row of the band
-  };
+template <int BN, int W, bool HB>
+struct EpiGradT {
+  typedef GradParams Params;
+  static constexpr bool kMultiTile = false;
+  static constexpr int FM = WaveCfg<W>::kFM;
   struct State {};
   static __device__ inline void assign(const GemmShape& g, const Params&, int bid, int nb, int& tm, int& t0,
                                        int& t1, int& split) {
@@ -322,53 +452,66 @@ struct EpiGrad {
     split = 0;
   }
   static __device__ inline void init(State&) {}
-  static __device__ inline void tile(const Params& p, State&, f32x4 (&acc)[4][BN / 32], const GemmShape& g,
-                                     int tm, int tn, int wm, int wn, int l) {
-    constexpr int FN = BN / 32;
+  static __device__ inline void tile(const Params& p, State&, WaveAcc<BN, W>& acc, const GemmShape& g, int tm,
+                                     int tn, int wm, int wn, int l) {
+    constexpr int FN = BN / 64;
+    pin_epilogue(l, tm, tn);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = tm * kBM + wm * 64 + i * 16 + (l & 15);
+    for (int i = 0; i < FM; ++i) {
+      const int m = tm * kBM + acc_row<W>(wm, i, l);
       if (m >= g.M) continue;
       const float4 rp = p.rowp[m];
       const int lab = p.rowlab[m] - p.v0;
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int cb = tn * BN + wn * (BN / 2) + j * 16 + (l >> 4) * 4;
-        float gv[4];
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int col = cb + r;
-          float gg = 0.f;
-          if (col < g.N) {
-            const float b = p.bias ? p.bias[p.v0 + col] : 0.f;
-            const float x = (acc[i][j][r] + b) * kLog2e - rp.x;
-            gg = rp.y * fast_exp2(x) - rp.w;
-            if (col == lab) gg -= rp.z;
+        for (int q = 0; q < 4; ++q) {
+          const int cb = tn * BN + acc_col<BN>(wn, j, q, l);
+          float gv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int col = cb + e;
+            float gg = 0.f;
+            if (col < g.N) {
+              const float b = HB ? p.bias[p.v0 + col] : 0.f;
+              const float x = (acc.v[i][j][4 * q + e] + b) * kLog2e - rp.x;
+              gg = rp.y * fast_exp2(x) - rp.w;
+              if (col == lab) gg -= rp.z;
+            }
+            gv[e] = gg;
           }
-          gv[r] = gg;
+          const u32x2 pk = {pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3])};
+          *reinterpret_cast<u32x2*>(p.G + (long)m * p.ldg + cb) = pk;
         }
-        const u32x2 pk = {pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3])};
-        *reinterpret_cast<u32x2*>(p.G + (long)m * p.ldg + cb) = pk;
-      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   static __device__ inline void finish(const Params&, State&, const GemmShape&, int, int, bf16_t*, int, int,
                                        int) {}
+};
+
+template <int BN, int W>
+using EpiGrad = EpiGradT<BN, W, false>;
+template <int BN, int W>
+using EpiGradBias = EpiGradT<BN, W, true>;
+
+struct AccParams {
+  float* acc32;
+  long ldacc;
+  void* out;
+  long ldo;
+  int out_f32;  // 0: bf16 output, 1: fp32 output
+  int mode;
 };
 
 // Plain GEMM output with optional fp32 accumulation buffer.
 //   mode 0: out = C            1: acc32 = C
 //   mode 2: acc32 += C          3: out = acc32 + C
-template <int BN>
+template <int BN, int W>
 struct EpiAcc {
-  struct Params {
-    float* acc32;
-    long ldacc;
-    void* out;
-    long ldo;
-    int out_f32;  // 0: bf16 output, 1: fp32 output
-    int mode;
-  };
+  typedef AccParams Params;
+  static constexpr bool kMultiTile = false;
+  static constexpr int FM = WaveCfg<W>::kFM;
   struct State {};
   static __device__ inline void assign(const GemmShape& g, const Params&, int bid, int nb, int& tm, int& t0,
                                        int& t1, int& split) {
@@ -380,28 +523,31 @@ struct EpiAcc {
     split = 0;
   }
   static __device__ inline void init(State&) {}
-  static __device__ inline void tile(const Params& p, State&, f32x4 (&acc)[4][BN / 32], const GemmShape& g,
-                                     int tm, int tn, int wm, int wn, int l) {
-    constexpr int FN = BN / 32;
+  static __device__ inline void tile(const Params& p, State&, WaveAcc<BN, W>& acc, const GemmShape& g, int tm,
+                                     int tn, int wm, int wn, int l) {
+    constexpr int FN = BN / 64;
+    pin_epilogue(l, tm, tn);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = tm * kBM + wm * 64 + i * 16 + (l & 15);
+    for (int i = 0; i < FM; ++i) {
+      const int m = tm * kBM + acc_row<W>(wm, i, l);
       if (m >= g.M) continue;
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int n = tn * BN + wn * (BN / 2) + j * 16 + (l >> 4) * 4;
-        if (n >= g.N) continue;
-        f32x4 v = acc[i][j];
-        if (p.mode >= 2) v += *reinterpret_cast<const f32x4*>(p.acc32 + (long)m * p.ldacc + n);
-        if (p.mode == 1 || p.mode == 2) {
-          *reinterpret_cast<f32x4*>(p.acc32 + (long)m * p.ldacc + n) = v;
-        } else if (p.out_f32) {
-          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + (long)m * p.ldo + n) = v;
-        } else {
-          const u32x2 pk = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-          *reinterpret_cast<u32x2*>(reinterpret_cast<bf16_t*>(p.out) + (long)m * p.ldo + n) = pk;
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = tn * BN + acc_col<BN>(wn, j, q, l);
+          if (n >= g.N) continue;
+          f32x4 v = {acc.v[i][j][4 * q], acc.v[i][j][4 * q + 1], acc.v[i][j][4 * q + 2], acc.v[i][j][4 * q + 3]};
+          if (p.mode >= 2) v += *reinterpret_cast<const f32x4*>(p.acc32 + (long)m * p.ldacc + n);
+          if (p.mode == 1 || p.mode == 2) {
+            *reinterpret_cast<f32x4*>(p.acc32 + (long)m * p.ldacc + n) = v;
+          } else if (p.out_f32) {
+            *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + (long)m * p.ldo + n) = v;
+          } else {
+            const u32x2 pk = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            *reinterpret_cast<u32x2*>(reinterpret_cast<bf16_t*>(p.out) + (long)m * p.ldo + n) = pk;
+          }
         }
-      }
     }
   }
   static __device__ inline void finish(const Params&, State&, const GemmShape&, int, int, bf16_t*, int, int,
@@ -409,15 +555,27 @@ struct EpiAcc {
 };
 
 // ---------------------------------------------------------------------------
-// The GEMM kernel: C[M,N] = A[M,K] . B[N,K]^T with a 2-stage LDS pipeline
-// (register-staged prefetch of slab s+1 while slab s feeds the MFMAs; one
-// barrier per slab).  A workgroup may own a run of column tiles (forward),
-// which the pipeline walks without draining between tiles.
+// The GEMM kernel: C[M,N] = A[M,K] . B[N,K]^T, 256 x BN x 64 tiles, two LDS
+// stages and two register sets of prefetched slabs.
+//
+// Software pipeline (per slab s, LDS stage p = s & 1):
+//   - global loads of slab s+2 go to register set p (issued unconditionally:
+//     past the last slab the loaders' bounds predicates read zeros, so the
+//     compiler's outstanding-load counts stay exact);
+//   - register set p^1 (slab s+1, loaded one slab earlier) drains into LDS
+//     stage p^1 after the first k-step;
+//   - the fragments of k-step kk+1 are read from LDS while the MFMAs of
+//     k-step kk run, and the first fragments of slab s+1 right after the
+//     barrier that closes slab s.
+// Tiles are walked in an even number of slabs (the loaders zero-fill past
+// K) so register-set and LDS-stage parities are static in the unrolled loop.
+// A workgroup may own a run of column tiles (forward); the pipeline then runs
+// on across tile boundaries.  Single-tile epilogues peel the last slab pair so
+// no prefetch registers are live while they run.
 // ---------------------------------------------------------------------------
-template <int BN, bool AK, bool BK, template <int> class EpiT>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmShape g, typename EpiT<BN>::Params ep) {
-  typedef EpiT<BN> Epi;
-  constexpr int FN = BN / 32;
+template <int BN, int W, bool AK, bool BKM, template <int, int> class EpiT, int PIPE>
+__global__ __launch_bounds__(W * 64) void gemm_kernel(GemmShape g, typename EpiT<BN, W>::Params ep) {
+  typedef EpiT<BN, W> Epi;
   constexpr int kStage = (kBM + BN) * kPitch;
   __shared__ __attribute__((aligned(16))) bf16_t smem[2 * kStage];
 
@@ -428,54 +586,124 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmShape g, typename Ep
   Epi::assign(g, ep, blockIdx.x, gridDim.x, tm, t0, t1, split);
   if (t0 >= t1) return;  // uniform for the whole workgroup
 
-  typename LoaderSel<AK, kBM>::type la;
-  typename LoaderSel<BK, BN>::type lb;
   typename Epi::State st;
   Epi::init(st);
-
-  f32x4 acc[4][FN];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  WaveAcc<BN, W> acc;
 
   const int KT = (g.K + kBK - 1) / kBK;
-  const int nsteps = (t1 - t0) * KT;
+  const int KT2 = (KT + 1) & ~1;
   const int a_r0 = tm * kBM;
+  bf16_t* const S0 = smem;
+  bf16_t* const S1 = smem + kStage;
 
-  // prologue: slab 0 of tile t0
-  la.load(g.A, g.lda, a_r0, g.M, 0, g.K, tid);
-  lb.load(g.B, g.ldb, t0 * BN, g.N, 0, g.K, tid);
-  la.store(smem, tid);
-  lb.store(smem + kBM * kPitch, tid);
-  __syncthreads();
-
-  int kt = 0, tn = t0;          // slab/tile being computed
-  int nkt = 1, ntn = t0;        // slab/tile being prefetched
-  if (nkt == KT) { nkt = 0; ++ntn; }
-  for (int s = 0; s < nsteps; ++s) {
-    const int cur = s & 1;
-    const bool more = (s + 1 < nsteps);
-    if (more) {
-      la.load(g.A, g.lda, a_r0, g.M, nkt * kBK, g.K, tid);
-      lb.load(g.B, g.ldb, ntn * BN, g.N, nkt * kBK, g.K, tid);
-    }
-    mma_slab<BN>(smem + cur * kStage, smem + cur * kStage + kBM * kPitch, acc, wm, wn, l);
-    if (more) {
-      la.store(smem + (cur ^ 1) * kStage, tid);
-      lb.store(smem + (cur ^ 1) * kStage + kBM * kPitch, tid);
-      if (++nkt == KT) { nkt = 0; ++ntn; }
-    }
+  if constexpr (PIPE == 1) {
+    // Simple pipeline: one slab in flight in registers, fragments read per
+    // k-step.  Its smaller register footprint suits 256-column tiles with 8
+    // waves, whose epilogue needs the room.
+    typename LoaderSel<AK, kBM, W>::type la;
+    typename LoaderSel<BKM, BN, W>::type lb;
+    la.load(g.A, g.lda, a_r0, g.M, 0, g.K, tid);
+    lb.load(g.B, g.ldb, t0 * BN, g.N, 0, g.K, tid);
+    la.store(S0, tid);
+    lb.store(S0 + kBM * kPitch, tid);
     __syncthreads();
-    if (++kt == KT) {
+    int s = 0;
+    for (int tn = t0; tn < t1; ++tn) {
+      acc.zero();
+      for (int kt = 0; kt < KT; ++kt, ++s) {
+        bf16_t* const Sc = (s & 1) ? S1 : S0;
+        bf16_t* const Sn = (s & 1) ? S0 : S1;
+        const bool last_k = (kt + 1 == KT);
+        const bool more = !(last_k && tn + 1 == t1);
+        if (more) {
+          const int nt = last_k ? tn + 1 : tn;
+          const int nk = last_k ? 0 : kt + 1;
+          la.load(g.A, g.lda, a_r0, g.M, nk * kBK, g.K, tid);
+          lb.load(g.B, g.ldb, nt * BN, g.N, nk * kBK, g.K, tid);
+        }
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          Frags<BN, W> f;
+          read_frags<BN, W>(Sc, Sc + kBM * kPitch, kk, f, wm, wn, l);
+          mfma_frags<BN, W>(f, acc);
+        }
+        if (more) {
+          la.store(Sn, tid);
+          lb.store(Sn + kBM * kPitch, tid);
+        }
+        __syncthreads();
+      }
       Epi::tile(ep, st, acc, g, tm, tn, wm, wn, l);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      kt = 0;
-      ++tn;
     }
+    Epi::finish(ep, st, g, tm, split, smem, wm, wn, l);
+    return;
+  }
+
+  typename LoaderSel<AK, kBM, W>::type la0, la1;
+  typename LoaderSel<BKM, BN, W>::type lb0, lb1;
+  Frags<BN, W> f0, f1;
+
+  // One slab on LDS stage P.  LOAD: refill register set P with slab (nt, nk).
+  // DRAIN: store register set P^1 into stage P^1.  SYNC: close the slab with
+  // a barrier and read the first fragments of the next slab.
+  auto slab = [&](auto P, auto LOAD, auto DRAIN, auto SYNC, int nt, int nk) {
+    constexpr int p = decltype(P)::value;
+    bf16_t* const Sc = p ? S1 : S0;
+    bf16_t* const Sn = p ? S0 : S1;
+    auto& la = [&]() -> auto& { if constexpr (p == 0) return la0; else return la1; }();
+    auto& lb = [&]() -> auto& { if constexpr (p == 0) return lb0; else return lb1; }();
+    auto& la_n = [&]() -> auto& { if constexpr (p == 0) return la1; else return la0; }();
+    auto& lb_n = [&]() -> auto& { if constexpr (p == 0) return lb1; else return lb0; }();
+    if constexpr (decltype(LOAD)::value) {
+      la.load(g.A, g.lda, a_r0, g.M, nk * kBK, g.K, tid);
+      lb.load(g.B, g.ldb, nt * BN, g.N, nk * kBK, g.K, tid);
+    }
+    read_frags<BN, W>(Sc, Sc + kBM * kPitch, 1, f1, wm, wn, l);
+    mfma_frags<BN, W>(f0, acc);
+    if constexpr (decltype(DRAIN)::value) {
+      la_n.store(Sn, tid);
+      lb_n.store(Sn + kBM * kPitch, tid);
+    }
+    read_frags<BN, W>(Sc, Sc + kBM * kPitch, 2, f0, wm, wn, l);
+    mfma_frags<BN, W>(f1, acc);
+    read_frags<BN, W>(Sc, Sc + kBM * kPitch, 3, f1, wm, wn, l);
+    mfma_frags<BN, W>(f0, acc);
+    mfma_frags<BN, W>(f1, acc);
+    __builtin_amdgcn_iglp_opt(0);
+    if constexpr (decltype(SYNC)::value) {
+      __syncthreads();
+      read_frags<BN, W>(Sn, Sn + kBM * kPitch, 0, f0, wm, wn, l);
+    }
+  };
+  typedef std::integral_constant<int, 0> I0;
+  typedef std::integral_constant<int, 1> I1;
+  typedef std::true_type T;
+  typedef std::false_type F;
+
+  // prologue: slabs 0 and 1 of tile t0 in flight, slab 0 in stage 0
+  la0.load(g.A, g.lda, a_r0, g.M, 0, g.K, tid);
+  lb0.load(g.B, g.ldb, t0 * BN, g.N, 0, g.K, tid);
+  la1.load(g.A, g.lda, a_r0, g.M, kBK, g.K, tid);
+  lb1.load(g.B, g.ldb, t0 * BN, g.N, kBK, g.K, tid);
+  la0.store(S0, tid);
+  lb0.store(S0 + kBM * kPitch, tid);
+  __syncthreads();
+  read_frags<BN, W>(S0, S0 + kBM * kPitch, 0, f0, wm, wn, l);
+
+  for (int tn = t0; tn < t1; ++tn) {
+    acc.zero();
+    const int kt_end = Epi::kMultiTile ? KT2 : KT2 - 2;
+    for (int kt = 0; kt < kt_end; kt += 2) {
+      const bool w0 = kt + 2 >= KT2, w1 = kt + 3 >= KT2;
+      slab(I0{}, T{}, T{}, T{}, w0 ? tn + 1 : tn, w0 ? kt + 2 - KT2 : kt + 2);
+      slab(I1{}, T{}, T{}, T{}, w1 ? tn + 1 : tn, w1 ? kt + 3 - KT2 : kt + 3);
+    }
+    if constexpr (!Epi::kMultiTile) {
+      // last slab pair of a single-tile workgroup: nothing left to load
+      slab(I0{}, F{}, T{}, T{}, 0, 0);
+      slab(I1{}, F{}, F{}, F{}, 0, 0);
+    }
+    Epi::tile(ep, st, acc, g, tm, tn, wm, wn, l);
   }
   Epi::finish(ep, st, g, tm, split, smem, wm, wn, l);
 }
@@ -728,7 +956,7 @@ struct Carver {
 // the 256 CUs several times over.
 int forward_splits(long N, long V) {
   if (N <= 0) return 1;
-  const long gm = ceil_div(N, kBM), tn = ceil_div(V, 256);
+  const long gm = ceil_div(N, kBM), tn = ceil_div(V, CCE_BN_LSE);
   long s = ceil_div(2048, gm);
   if (s > tn) s = tn;
   if (s < 1) s = 1;
@@ -800,10 +1028,10 @@ int check_dims(long N, long d, long V) {
   return CCE_OK;
 }
 
-template <int BN, bool AK, bool BK, template <int> class EpiT>
-int launch_gemm(const GemmShape& g, const typename EpiT<BN>::Params& ep, int nblocks, hipStream_t st) {
+template <int BN, int W, bool AK, bool BK, template <int, int> class EpiT, int PIPE = 3>
+int launch_gemm(const GemmShape& g, const typename EpiT<BN, W>::Params& ep, int nblocks, hipStream_t st) {
   if (nblocks <= 0) return CCE_OK;
-  hipLaunchKernelGGL((gemm_kernel<BN, AK, BK, EpiT>), dim3(nblocks), dim3(kThreads), 0, st, g, ep);
+  hipLaunchKernelGGL((gemm_kernel<BN, W, AK, BK, EpiT, PIPE>), dim3(nblocks), dim3(W * 64), 0, st, g, ep);
   HIP_TRY(hipGetLastError());
   return CCE_OK;
 }
@@ -820,23 +1048,11 @@ int zero_fill(void* p, size_t bytes, hipStream_t st) {
   return CCE_OK;
 }
 
-// Band GEMM for dH / dW: pick the column tile that wastes least of d.
-bool use_bn256(long d) { return (align_up((size_t)d, 256) - d) <= (align_up((size_t)d, 128) - d); }
 
-template <int BN>
-int launch_dh(const GemmShape& g, const EpiAcc<256>::Params& ep, hipStream_t st) {
+template <int BN, bool AK>
+int launch_acc(const GemmShape& g, const AccParams& ep, hipStream_t st) {
   const int nb = (int)(ceil_div(g.M, kBM) * ceil_div(g.N, BN));
-  typename EpiAcc<BN>::Params p;
-  p.acc32 = ep.acc32; p.ldacc = ep.ldacc; p.out = ep.out; p.ldo = ep.ldo; p.out_f32 = ep.out_f32; p.mode = ep.mode;
-  return launch_gemm<BN, true, true, EpiAcc>(g, p, nb, st);
-}
-
-template <int BN>
-int launch_dw(const GemmShape& g, const EpiAcc<256>::Params& ep, hipStream_t st) {
-  const int nb = (int)(ceil_div(g.M, kBM) * ceil_div(g.N, BN));
-  typename EpiAcc<BN>::Params p;
-  p.acc32 = ep.acc32; p.ldacc = ep.ldacc; p.out = ep.out; p.ldo = ep.ldo; p.out_f32 = ep.out_f32; p.mode = ep.mode;
-  return launch_gemm<BN, false, true, EpiAcc>(g, p, nb, st);
+  return launch_gemm<BN, CCE_W_ACC, AK, true, EpiAcc>(g, ep, nb, st);
 }
 
 }  // namespace
@@ -910,13 +1126,14 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
   g.M = (int)N;
   g.N = (int)V;
   g.K = (int)d;
-  EpiLse<256>::Params ep;
+  LseParams ep;
   ep.bias = bias;
   ep.pm = L.pm;
   ep.ps = L.ps;
   ep.splits = S;
-  ep.tiles_n = (int)ceil_div(V, 256);
-  rc = launch_gemm<256, true, true, EpiLse>(g, ep, gm * S, st);
+  ep.tiles_n = (int)ceil_div(V, CCE_BN_LSE);
+  rc = bias ? launch_gemm<CCE_BN_LSE, CCE_W_LSE, true, true, EpiLseBias, CCE_PIPE_LSE>(g, ep, gm * S, st)
+            : launch_gemm<CCE_BN_LSE, CCE_W_LSE, true, true, EpiLse, CCE_PIPE_LSE>(g, ep, gm * S, st);
   if (rc) return rc;
 
   const int nb = (int)ceil_div(N, 4);
@@ -995,9 +1212,11 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     GemmShape g1;
     g1.A = H; g1.lda = d; g1.B = W + v0 * d; g1.ldb = d;
     g1.M = (int)N; g1.N = (int)vb; g1.K = (int)d;
-    EpiGrad<256>::Params e1;
+    GradParams e1;
     e1.bias = bias; e1.rowp = L.rowp; e1.rowlab = L.rowlab; e1.G = L.G; e1.ldg = Vb; e1.v0 = (int)v0;
-    rc = launch_gemm<256, true, true, EpiGrad>(g1, e1, gm * (int)ceil_div(vb, 256), st);
+    const int nb1 = gm * (int)ceil_div(vb, CCE_BN_GRAD);
+    rc = bias ? launch_gemm<CCE_BN_GRAD, CCE_W_GRAD, true, true, EpiGradBias, CCE_PIPE_GRAD>(g1, e1, nb1, st)
+              : launch_gemm<CCE_BN_GRAD, CCE_W_GRAD, true, true, EpiGrad, CCE_PIPE_GRAD>(g1, e1, nb1, st);
     if (rc) return rc;
 
     if (need_dh) {
@@ -1008,11 +1227,11 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       GemmShape g2;
       g2.A = L.G; g2.lda = Vb; g2.B = L.WT; g2.ldb = Vb;
       g2.M = (int)N; g2.N = (int)d; g2.K = (int)vb64;
-      EpiAcc<256>::Params e2;
+      AccParams e2;
       e2.acc32 = L.dHacc; e2.ldacc = d; e2.out = grad_hidden; e2.ldo = d;
       e2.out_f32 = (grad_hidden_dtype == CCE_DTYPE_F32);
       e2.mode = (nbands == 1) ? 0 : (b == 0 ? 1 : (b == nbands - 1 ? 3 : 2));
-      rc = use_bn256(d) ? launch_dh<256>(g2, e2, st) : launch_dh<128>(g2, e2, st);
+      rc = launch_acc<128, true>(g2, e2, st);
       if (rc) return rc;
     }
     if (need_dw) {
@@ -1020,7 +1239,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       g3.A = L.G; g3.lda = Vb;  // MN-major: element (v, n) at G[n*Vb + v]
       g3.B = L.HT; g3.ldb = N8;
       g3.M = (int)vb; g3.N = (int)d; g3.K = (int)N;
-      EpiAcc<256>::Params e3;
+      AccParams e3;
       e3.acc32 = nullptr; e3.ldacc = 0;
       e3.out = (grad_weight_dtype == CCE_DTYPE_F32)
                    ? static_cast<void*>(static_cast<float*>(grad_weight) + v0 * d)
@@ -1028,7 +1247,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       e3.ldo = d;
       e3.out_f32 = (grad_weight_dtype == CCE_DTYPE_F32);
       e3.mode = 0;
-      rc = use_bn256(d) ? launch_dw<256>(g3, e3, st) : launch_dw<128>(g3, e3, st);
+      rc = launch_acc<128, false>(g3, e3, st);
       if (rc) return rc;
     }
     if (need_db) {
