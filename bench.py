@@ -2,8 +2,14 @@
 
 Default workload is BASELINE config C2 (Qwen2.5-0.5B-shaped head: N=16384,
 d=896, V=151936, bf16, 5% ignore_index, mean).  A step is one
-cut_cross_entropy forward plus backward producing dHidden and dW.  Prints one
-JSON line (the driver's contract).
+cut_cross_entropy forward plus backward producing dHidden and dW, with the
+inputs already resident in HBM.  Prints one JSON line (the driver's contract).
+
+Roofline: the dominant credited kernel (the largest share of step time among
+the forward GEMM, the dHidden GEMM and the dW GEMM; the logits recompute is not
+credited, as the algorithmic work of a fwd+bwd step is 6*N*V*d FLOPs) is timed
+with HIP events on its own launch stream by the library
+(cce_kernel_timing_enable) over the timed region.
 """
 from __future__ import annotations
 
@@ -21,6 +27,7 @@ if REPO not in sys.path:
 
 PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 4096 FLOP/clk x 2.4 GHz (dense bf16 MFMA)
 PEAK_HBM_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 
 
 def cpu_model() -> str:
@@ -36,9 +43,6 @@ def cpu_model() -> str:
 
 def cpu_baseline(cfg, rows: int, seed: int = 0) -> dict:
     """Oracle (numpy restatement of the reference CPU path) fwd+bwd on a row slice; tokens/s."""
-    import numpy as np
-    import torch
-
     from oracle import cce_oracle
     from tests.cce_common import make_inputs
 
@@ -47,18 +51,32 @@ def cpu_baseline(cfg, rows: int, seed: int = 0) -> dict:
     wn = w.float().numpy()
     ln = lab.numpy()
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    cce_oracle.loss_and_grads(hn[: max(8, rows // 8)], wn, ln[: max(8, rows // 8)], chunk_size=8192)  # warm-up
+    warm = max(8, rows // 8)
+    cce_oracle.loss_and_grads(hn[:warm], wn, ln[:warm], chunk_size=8192)
     times = []
     for _ in range(3):
         t0 = time.perf_counter()
         cce_oracle.loss_and_grads(hn, wn, ln, chunk_size=8192)
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
-    del torch
     return {"value": rows / t, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{cfg.name} rows[:{rows}] of N={cfg.N} (full d={cfg.d}, V={cfg.V}), fp32 numpy, "
-                      f"median of 3 after a warm-up, {t:.2f} s per run; extrapolated linearly in N",
+            "sample": f"{cfg.name} rows[:{rows}] of N={cfg.N} (full d={cfg.d}, V={cfg.V}); fp32 numpy/BLAS "
+                      f"restatement of the reference CPU path (V-chunk 8192); median of 3 runs after a warm-up, "
+                      f"{t:.2f} s per run; tokens/s = rows / time (linear in N)",
             "cpu": cpu_model()}
+
+
+def copy_calibration(nbytes: int) -> None:
+    """A plain device copy of known size, for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "launches": 3}), flush=True)
 
 
 def main() -> int:
@@ -68,17 +86,23 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="C2")
     ap.add_argument("--chunk", type=int, default=8192)
-    ap.add_argument("--cpu-rows", type=int, default=512)
+    ap.add_argument("--cpu-rows", type=int, default=4096)
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device copy of BYTES (PMC calibration) and exit")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs the fused linear-CE path on a single MI355X "
               "(use --gpus 1)", file=sys.stderr)
         return 2
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return 0
 
     import torch
 
+    from chronicals_amd import _lib
     from chronicals_amd.kernels.cut_cross_entropy import cut_cross_entropy
     from tests.cce_common import CONFIGS, make_inputs
 
@@ -100,25 +124,56 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    for k in range(_lib.CCE_KERNEL_KINDS):
+        _lib.kernel_timing_read(k)  # drop anything recorded so far
     base_mem = torch.cuda.memory_allocated()
     torch.cuda.reset_peak_memory_stats()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
+    _lib.kernel_timing_enable(True)
     torch.cuda.synchronize()
     start.record()
     for _ in range(args.steps):
         loss = step()
     end.record()
     torch.cuda.synchronize()
+    _lib.kernel_timing_enable(False)
     ms = start.elapsed_time(end) / args.steps
     peak_extra = torch.cuda.max_memory_allocated() - base_mem
 
-    flops = 6.0 * N * V * d
-    achieved = flops / (ms * 1e-3) / 1e12
-    tokens_per_s = N / (ms * 1e-3)
+    # per-kernel breakdown; algorithmic FLOPs per step of each credited kernel = 2*N*V*d
+    flops_2nvd = 2.0 * N * V * d
+    kernels = {}
+    for k, name in _lib.KERNEL_KIND_NAMES.items():
+        tot_ms, n = _lib.kernel_timing_read(k)
+        if n == 0:
+            continue
+        avg_ms = tot_ms / n
+        per_step = n / args.steps
+        kernels[name] = {
+            "launches_per_step": per_step,
+            "avg_launch_us": avg_ms * 1e3,
+            "ms_per_step": tot_ms / args.steps,
+            # executed MFMA work per launch (the recompute executes 2*N*V*d too)
+            "tflops_executed": (flops_2nvd / per_step) / (avg_ms * 1e-3) / 1e12,
+        }
+    credited = [k for k in ("fwd_lse", "bwd_dh", "bwd_dw") if k in kernels]
+    dom = max(credited, key=lambda k: kernels[k]["ms_per_step"])
+    kd = kernels[dom]
+    achieved = kd["tflops_executed"]
+    traffic = None
+    try:
+        with open(TRAFFIC_FILE) as f:
+            tr = json.load(f)
+        if tr.get("config") == cfg.name and tr.get("kernel") == dom:
+            traffic = tr.get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        pass
+
+    step_tflops = 6.0 * N * V * d / (ms * 1e-3) / 1e12
     out = {
         "metric": "fused linear-CE fwd+bwd tokens/s and % bf16 MFMA peak, N=16k V=152k",
-        "value": tokens_per_s,
+        "value": N / (ms * 1e-3),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -128,14 +183,18 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) hidden, N(0,0.02) W, uniform labels)",
+        "data": "synthetic (seeded N(0,1) hidden, N(0,0.02) W, uniform labels, 5% ignore_index)",
         "config": {"workload": f"{cfg.name}: fused linear-CE fwd+bwd N={N} d={d} V={V} bf16, "
-                               f"{int(cfg.ignore_frac * 100)}% ignore_index, {cfg.reduction}",
+                               f"{int(cfg.ignore_frac * 100)}% ignore_index, {cfg.reduction}; grads dHidden, dW",
                    "N": N, "d": d, "V": V, "chunk_size": args.chunk},
-        "pct_bf16_peak": 100.0 * achieved / PEAK_BF16_TFLOPS,
+        "pct_bf16_peak": 100.0 * step_tflops / PEAK_BF16_TFLOPS,
+        "step_tflops_algorithmic": step_tflops,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
-                     "kernel": "whole fwd+bwd step (6*N*V*d algorithmic FLOPs)"},
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
+                     "kernel": f"{dom}: 2*N*V*d/launches_per_step FLOPs per launch over its HIP-event "
+                               f"average launch time ({kd['avg_launch_us']:.1f} us, "
+                               f"{kd['launches_per_step']:g} launches/step)"},
+        "kernels": kernels,
         "peak_extra_mem_bytes": int(peak_extra),
         "loss": float(loss.item()),
     }

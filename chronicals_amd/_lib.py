@@ -22,6 +22,14 @@ CCE_REDUCTION_SUM = 2
 CCE_DTYPE_BF16 = 0
 CCE_DTYPE_F32 = 1
 
+CCE_KERNEL_FWD_LSE = 0
+CCE_KERNEL_BWD_GRAD = 1
+CCE_KERNEL_BWD_DH = 2
+CCE_KERNEL_BWD_DW = 3
+CCE_KERNEL_KINDS = 4
+KERNEL_KIND_NAMES = {CCE_KERNEL_FWD_LSE: "fwd_lse", CCE_KERNEL_BWD_GRAD: "bwd_grad", CCE_KERNEL_BWD_DH: "bwd_dh",
+                     CCE_KERNEL_BWD_DW: "bwd_dw"}
+
 REDUCTIONS = {"none": CCE_REDUCTION_NONE, "mean": CCE_REDUCTION_MEAN, "sum": CCE_REDUCTION_SUM}
 
 _vp = ctypes.c_void_p
@@ -51,6 +59,8 @@ SIGNATURES = {
         _vp, _i32, _vp, _i32, _vp,           # grad_hidden, dtype, grad_weight, dtype, grad_bias
         _vp, _sz, _vp,                       # workspace, workspace_bytes, stream
     ]),
+    "cce_kernel_timing_enable": (_i32, [_i32]),
+    "cce_kernel_timing_read": (_i32, [_i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64)]),
 }
 
 _lock = threading.Lock()
@@ -107,3 +117,15 @@ def backward_workspace_bytes(N: int, d: int, V: int, chunk_size: int, need_dh: b
     out = _sz(0)
     check(load().cce_backward_workspace_bytes(N, d, V, chunk_size, int(need_dh), int(need_dw), ctypes.byref(out)))
     return out.value
+
+
+def kernel_timing_enable(enable: bool) -> None:
+    check(load().cce_kernel_timing_enable(int(enable)))
+
+
+def kernel_timing_read(kind: int):
+    """(total milliseconds, launches) recorded for one kernel kind since the last read."""
+    ms = ctypes.c_double(0.0)
+    n = _i64(0)
+    check(load().cce_kernel_timing_read(kind, ctypes.byref(ms), ctypes.byref(n)))
+    return ms.value, n.value

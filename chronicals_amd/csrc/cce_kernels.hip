@@ -35,7 +35,9 @@
 #include <math.h>
 #include <float.h>
 
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "../../include/chronicals_cce.h"
 
@@ -1028,11 +1030,49 @@ int check_dims(long N, long d, long V) {
   return CCE_OK;
 }
 
+// Optional per-kind kernel timing (cce_kernel_timing_enable).
+struct KernelTiming {
+  std::mutex mu;
+  bool enabled = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pending[CCE_KERNEL_KINDS];
+  std::vector<hipEvent_t> pool;
+  hipEvent_t get() {
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+};
+KernelTiming g_timing;
+
+// Records the start event of a timed launch; returns false when timing is off.
+bool timing_begin(hipStream_t st, hipEvent_t* ev0, hipEvent_t* ev1) {
+  std::lock_guard<std::mutex> lk(g_timing.mu);
+  if (!g_timing.enabled) return false;
+  *ev0 = g_timing.get();
+  *ev1 = g_timing.get();
+  if (!*ev0 || !*ev1) return false;
+  return hipEventRecord(*ev0, st) == hipSuccess;
+}
+
+void timing_end(int kind, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+  std::lock_guard<std::mutex> lk(g_timing.mu);
+  if (hipEventRecord(ev1, st) == hipSuccess) g_timing.pending[kind].emplace_back(ev0, ev1);
+}
+
 template <int BN, int W, bool AK, bool BK, template <int, int> class EpiT, int PIPE = 3>
-int launch_gemm(const GemmShape& g, const typename EpiT<BN, W>::Params& ep, int nblocks, hipStream_t st) {
+int launch_gemm(const GemmShape& g, const typename EpiT<BN, W>::Params& ep, int nblocks, hipStream_t st,
+                int kind) {
   if (nblocks <= 0) return CCE_OK;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  const bool timed = timing_begin(st, &e0, &e1);
   hipLaunchKernelGGL((gemm_kernel<BN, W, AK, BK, EpiT, PIPE>), dim3(nblocks), dim3(W * 64), 0, st, g, ep);
   HIP_TRY(hipGetLastError());
+  if (timed) timing_end(kind, st, e0, e1);
   return CCE_OK;
 }
 
@@ -1050,9 +1090,9 @@ int zero_fill(void* p, size_t bytes, hipStream_t st) {
 
 
 template <int BN, bool AK>
-int launch_acc(const GemmShape& g, const AccParams& ep, hipStream_t st) {
+int launch_acc(const GemmShape& g, const AccParams& ep, hipStream_t st, int kind) {
   const int nb = (int)(ceil_div(g.M, kBM) * ceil_div(g.N, BN));
-  return launch_gemm<BN, CCE_W_ACC, AK, true, EpiAcc>(g, ep, nb, st);
+  return launch_gemm<BN, CCE_W_ACC, AK, true, EpiAcc>(g, ep, nb, st, kind);
 }
 
 }  // namespace
@@ -1132,8 +1172,10 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
   ep.ps = L.ps;
   ep.splits = S;
   ep.tiles_n = (int)ceil_div(V, CCE_BN_LSE);
-  rc = bias ? launch_gemm<CCE_BN_LSE, CCE_W_LSE, true, true, EpiLseBias, CCE_PIPE_LSE>(g, ep, gm * S, st)
-            : launch_gemm<CCE_BN_LSE, CCE_W_LSE, true, true, EpiLse, CCE_PIPE_LSE>(g, ep, gm * S, st);
+  rc = bias ? launch_gemm<CCE_BN_LSE, CCE_W_LSE, true, true, EpiLseBias, CCE_PIPE_LSE>(g, ep, gm * S, st,
+                                                                                      CCE_KERNEL_FWD_LSE)
+            : launch_gemm<CCE_BN_LSE, CCE_W_LSE, true, true, EpiLse, CCE_PIPE_LSE>(g, ep, gm * S, st,
+                                                                                  CCE_KERNEL_FWD_LSE);
   if (rc) return rc;
 
   const int nb = (int)ceil_div(N, 4);
@@ -1215,8 +1257,10 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     GradParams e1;
     e1.bias = bias; e1.rowp = L.rowp; e1.rowlab = L.rowlab; e1.G = L.G; e1.ldg = Vb; e1.v0 = (int)v0;
     const int nb1 = gm * (int)ceil_div(vb, CCE_BN_GRAD);
-    rc = bias ? launch_gemm<CCE_BN_GRAD, CCE_W_GRAD, true, true, EpiGradBias, CCE_PIPE_GRAD>(g1, e1, nb1, st)
-              : launch_gemm<CCE_BN_GRAD, CCE_W_GRAD, true, true, EpiGrad, CCE_PIPE_GRAD>(g1, e1, nb1, st);
+    rc = bias ? launch_gemm<CCE_BN_GRAD, CCE_W_GRAD, true, true, EpiGradBias, CCE_PIPE_GRAD>(g1, e1, nb1, st,
+                                                                                           CCE_KERNEL_BWD_GRAD)
+              : launch_gemm<CCE_BN_GRAD, CCE_W_GRAD, true, true, EpiGrad, CCE_PIPE_GRAD>(g1, e1, nb1, st,
+                                                                                       CCE_KERNEL_BWD_GRAD);
     if (rc) return rc;
 
     if (need_dh) {
@@ -1231,7 +1275,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       e2.acc32 = L.dHacc; e2.ldacc = d; e2.out = grad_hidden; e2.ldo = d;
       e2.out_f32 = (grad_hidden_dtype == CCE_DTYPE_F32);
       e2.mode = (nbands == 1) ? 0 : (b == 0 ? 1 : (b == nbands - 1 ? 3 : 2));
-      rc = launch_acc<128, true>(g2, e2, st);
+      rc = launch_acc<128, true>(g2, e2, st, CCE_KERNEL_BWD_DH);
       if (rc) return rc;
     }
     if (need_dw) {
@@ -1247,7 +1291,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       e3.ldo = d;
       e3.out_f32 = (grad_weight_dtype == CCE_DTYPE_F32);
       e3.mode = 0;
-      rc = launch_acc<128, false>(g3, e3, st);
+      rc = launch_acc<128, false>(g3, e3, st, CCE_KERNEL_BWD_DW);
       if (rc) return rc;
     }
     if (need_db) {
@@ -1257,6 +1301,45 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     }
   }
   return CCE_OK;
+}
+
+int cce_kernel_timing_enable(int enable) {
+  g_err[0] = 0;
+  std::lock_guard<std::mutex> lk(g_timing.mu);
+  g_timing.enabled = enable != 0;
+  return CCE_OK;
+}
+
+int cce_kernel_timing_read(int kind, double* total_ms, int64_t* launches) {
+  g_err[0] = 0;
+  if (kind < 0 || kind >= CCE_KERNEL_KINDS) return fail(CCE_ERR_INVALID_ARG, "kernel kind %d out of range", kind);
+  if (!total_ms || !launches) return fail(CCE_ERR_INVALID_ARG, "total_ms and launches must not be null");
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> recs;
+  {
+    std::lock_guard<std::mutex> lk(g_timing.mu);
+    recs.swap(g_timing.pending[kind]);
+  }
+  double sum = 0.0;
+  int rc = CCE_OK;
+  for (auto& r : recs) {
+    float ms = 0.f;
+    if (rc == CCE_OK) {
+      hipError_t e = hipEventSynchronize(r.second);
+      if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.first, r.second);
+      if (e != hipSuccess) rc = fail(CCE_ERR_HIP, "kernel timing: %s", hipGetErrorString(e));
+    }
+    sum += ms;
+  }
+  {
+    std::lock_guard<std::mutex> lk(g_timing.mu);
+    for (auto& r : recs) {
+      g_timing.pool.push_back(r.first);
+      g_timing.pool.push_back(r.second);
+    }
+  }
+  *total_ms = sum;
+  *launches = (int64_t)recs.size();
+  return rc;
 }
 
 }  // extern "C"

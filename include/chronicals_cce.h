@@ -106,6 +106,21 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
                  int grad_hidden_dtype, void* grad_weight, int grad_weight_dtype, float* grad_bias,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Per-kernel timing for measurement tools (no counterpart in the reference).
+ * While enabled, every GEMM launch of cce_forward / cce_backward is bracketed
+ * by HIP events recorded on its stream.  cce_kernel_timing_read() waits for
+ * the recorded events, returns the summed milliseconds and launch count of
+ * one kernel kind and clears that kind's record.  Kinds:
+ */
+#define CCE_KERNEL_FWD_LSE 0   /* forward GEMM + online logsumexp        */
+#define CCE_KERNEL_BWD_GRAD 1  /* backward recompute GEMM -> dLoss/dS     */
+#define CCE_KERNEL_BWD_DH 2    /* dHidden GEMM (per vocabulary band)      */
+#define CCE_KERNEL_BWD_DW 3    /* dWeight GEMM (per vocabulary band)      */
+#define CCE_KERNEL_KINDS 4
+int cce_kernel_timing_enable(int enable);
+int cce_kernel_timing_read(int kind, double* total_ms, int64_t* launches);
+
 #ifdef __cplusplus
 }
 #endif
