@@ -6,8 +6,9 @@ cut_cross_entropy forward plus backward producing dHidden and dW, with the
 inputs already resident in HBM.  Prints one JSON line (the driver's contract).
 
 Roofline: the dominant credited kernel (the largest share of step time among
-the forward GEMM, the dHidden GEMM and the dW GEMM; the logits recompute is not
-credited, as the algorithmic work of a fwd+bwd step is 6*N*V*d FLOPs) is timed
+the forward GEMM and the dHidden/dW GEMMs, which run as one launch per band
+when both gradients are needed; the logits recompute is not credited, as the
+algorithmic work of a fwd+bwd step is 6*N*V*d FLOPs) is timed
 with HIP events on its own launch stream by the library
 (cce_kernel_timing_enable) over the timed region.
 """
@@ -150,14 +151,15 @@ def main() -> int:
             continue
         avg_ms = tot_ms / n
         per_step = n / args.steps
+        step_flops = 2 * flops_2nvd if name == "bwd_dhdw" else flops_2nvd  # dH + dW share one launch
         kernels[name] = {
             "launches_per_step": per_step,
             "avg_launch_us": avg_ms * 1e3,
             "ms_per_step": tot_ms / args.steps,
             # executed MFMA work per launch (the recompute executes 2*N*V*d too)
-            "tflops_executed": (flops_2nvd / per_step) / (avg_ms * 1e-3) / 1e12,
+            "tflops_executed": (step_flops / per_step) / (avg_ms * 1e-3) / 1e12,
         }
-    credited = [k for k in ("fwd_lse", "bwd_dh", "bwd_dw") if k in kernels]
+    credited = [k for k in ("fwd_lse", "bwd_dh", "bwd_dw", "bwd_dhdw") if k in kernels]
     dom = max(credited, key=lambda k: kernels[k]["ms_per_step"])
     kd = kernels[dom]
     achieved = kd["tflops_executed"]
@@ -191,7 +193,8 @@ def main() -> int:
         "step_tflops_algorithmic": step_tflops,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
-                     "kernel": f"{dom}: 2*N*V*d/launches_per_step FLOPs per launch over its HIP-event "
+                     "kernel": f"{dom}: {'4' if dom == 'bwd_dhdw' else '2'}*N*V*d/launches_per_step FLOPs per "
+                               f"launch over its HIP-event "
                                f"average launch time ({kd['avg_launch_us']:.1f} us, "
                                f"{kd['launches_per_step']:g} launches/step)"},
         "kernels": kernels,

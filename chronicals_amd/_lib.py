@@ -26,9 +26,10 @@ CCE_KERNEL_FWD_LSE = 0
 CCE_KERNEL_BWD_GRAD = 1
 CCE_KERNEL_BWD_DH = 2
 CCE_KERNEL_BWD_DW = 3
-CCE_KERNEL_KINDS = 4
+CCE_KERNEL_BWD_DHDW = 4
+CCE_KERNEL_KINDS = 5
 KERNEL_KIND_NAMES = {CCE_KERNEL_FWD_LSE: "fwd_lse", CCE_KERNEL_BWD_GRAD: "bwd_grad", CCE_KERNEL_BWD_DH: "bwd_dh",
-                     CCE_KERNEL_BWD_DW: "bwd_dw"}
+                     CCE_KERNEL_BWD_DW: "bwd_dw", CCE_KERNEL_BWD_DHDW: "bwd_dhdw"}
 
 REDUCTIONS = {"none": CCE_REDUCTION_NONE, "mean": CCE_REDUCTION_MEAN, "sum": CCE_REDUCTION_SUM}
 

@@ -35,6 +35,7 @@
 #include <math.h>
 #include <float.h>
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -50,28 +51,15 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// Per-GEMM configuration (wave layout W, column tile BN, pipeline PIPE);
-// overridable at build time for tuning.
-#ifndef CCE_W_LSE
-#define CCE_W_LSE 8
-#endif
-#ifndef CCE_W_GRAD
-#define CCE_W_GRAD 8
-#endif
-#ifndef CCE_W_ACC
-#define CCE_W_ACC 8
-#endif
-#ifndef CCE_BN_LSE
-#define CCE_BN_LSE 128
-#endif
-#ifndef CCE_BN_GRAD
-#define CCE_BN_GRAD 256
-#endif
-#ifndef CCE_PIPE_GRAD
-#define CCE_PIPE_GRAD 1
-#endif
-#ifndef CCE_PIPE_LSE
-#define CCE_PIPE_LSE 3
+// Per-GEMM configuration: wave layout W (8 or 4), column tile BN and main-loop
+// pipeline PIPE (4: direct-to-LDS loads, needs K-major operands with K a
+// multiple of 64; 3: register-staged loads, any K; 1: simple register
+// pipeline).  The "fallback" configuration serves K % 64 != 0.
+constexpr int kWarp8 = 8;
+constexpr int kFastBN = 256;    // PIPE 4 kernels
+constexpr int kSlowBN = 128;    // PIPE 3 kernels
+#ifndef CCE_GRAD_WGS
+#define CCE_GRAD_WGS 1024  // target workgroups of a recompute launch
 #endif
 
 constexpr int kBM = 256;              // rows of a workgroup tile
@@ -266,6 +254,43 @@ __device__ inline void pin_epilogue(int& l, int& tm, int& tn) {
   asm volatile("" : "+s"(tm), "+s"(tn));
 }
 
+// ---------------------------------------------------------------------------
+// Direct global -> LDS loads (PIPE 4).  A buffer load with the `lds` modifier
+// writes each lane's 16 bytes straight into LDS at M0 + 16*lane, so one wave
+// instruction fills 1 KB = 8 rows x 128 B of a [row][64 k] tile.  LDS rows
+// are not padded; instead the 16-byte chunk c of row r lives at physical chunk
+// c ^ swz(r), which keeps the MFMA fragment reads (16 or 8 lanes per phase,
+// 32 consecutive rows, one chunk) on distinct banks.  Rows past the operand's
+// end fall outside the buffer descriptor's range and read as zero; the
+// epilogues mask them in any case.
+// ---------------------------------------------------------------------------
+__device__ inline int swz(int r) { return (r ^ (r >> 3)) & 7; }
+
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, long bytes) {
+  const long cap = 0x7ffffff0L;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)(bytes < cap ? bytes : cap),
+                                           0x00020000);
+}
+
+// Issue the DMA of a K-major tile: rows [r0, r0 + BR) x k [k0, k0 + 64) into
+// the swizzled LDS region S.  K must be a multiple of 64 (no K tail).
+template <int BR, int W>
+__device__ inline void dma_kmajor(const bf16_t* __restrict__ X, long ld, int r0, int rlim, int k0, bf16_t* S,
+                                  int w, int l) {
+  constexpr int kI = BR / (8 * W);  // wave instructions per wave
+  const long rows_left = (long)rlim - r0;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(X + (long)r0 * ld, rows_left > 0 ? rows_left * ld * 2 : 0);
+#pragma unroll
+  for (int j = 0; j < kI; ++j) {
+    const int blk = w * kI + j;           // 8-row block of the tile
+    const int row = blk * 8 + (l >> 3);
+    const int c = (l & 7) ^ swz(row);     // logical chunk this lane fetches
+    const int voff = (int)(((long)row * ld + c * 8) * 2);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rs, (__attribute__((address_space(3))) void*)(S + blk * 512), 16, voff, k0 * 2, 0, 0);
+  }
+}
+
 // Register fragments of one k-step (16 of K) for a wave.
 template <int BN, int W>
 struct Frags {
@@ -282,6 +307,23 @@ __device__ inline void read_frags(const bf16_t* __restrict__ As, const bf16_t* _
 #pragma unroll
   for (int j = 0; j < BN / 64; ++j)
     f.b[j] = *reinterpret_cast<const u32x4*>(Bs + (wn * (BN / 2) + j * 32 + (l & 31)) * kPitch + kof);
+}
+
+// Fragment reads from the swizzled (unpadded, 64 bf16 per row) layout.
+template <int BN, int W>
+__device__ inline void read_frags_swz(const bf16_t* __restrict__ As, const bf16_t* __restrict__ Bs, int kk,
+                                      Frags<BN, W>& f, int wm, int wn, int l) {
+  const int c = kk * 2 + (l >> 5);
+#pragma unroll
+  for (int i = 0; i < WaveCfg<W>::kFM; ++i) {
+    const int r = wm * WaveCfg<W>::kWaveRows + i * 32 + (l & 31);
+    f.a[i] = *reinterpret_cast<const u32x4*>(As + r * 64 + ((c ^ swz(r)) << 3));
+  }
+#pragma unroll
+  for (int j = 0; j < BN / 64; ++j) {
+    const int r = wn * (BN / 2) + j * 32 + (l & 31);
+    f.b[j] = *reinterpret_cast<const u32x4*>(Bs + r * 64 + ((c ^ swz(r)) << 3));
+  }
 }
 
 // v_mfma_f32_32x32x16_bf16 over the kFM x (BN/64) blocks of one k-step.
@@ -434,6 +476,8 @@ struct GradParams {
   bf16_t* G;             // [M][ldg]
   long ldg;
   int v0;                // first vocabulary row of the band
+  int splits;            // column-tile runs per row tile
+  int tiles_n;           // column tiles in the band
 };
 
 // Backward recompute: G[n][c] = dLoss/dS for one vocabulary band, stored bf16.
@@ -441,17 +485,19 @@ struct GradParams {
 template <int BN, int W, bool HB>
 struct EpiGradT {
   typedef GradParams Params;
-  static constexpr bool kMultiTile = false;
+  // Each workgroup walks a run of column tiles of one row tile, so the next
+  // tile's loads are in flight while this tile's epilogue runs.
+  static constexpr bool kMultiTile = true;
   static constexpr int FM = WaveCfg<W>::kFM;
   struct State {};
-  static __device__ inline void assign(const GemmShape& g, const Params&, int bid, int nb, int& tm, int& t0,
+  static __device__ inline void assign(const GemmShape& g, const Params& p, int bid, int nb, int& tm, int& t0,
                                        int& t1, int& split) {
-    const int gm = (g.M + kBM - 1) / kBM, gn = (g.N + BN - 1) / BN;
-    int tn;
-    grouped_map(bid, nb, gm, gn, tm, tn);
-    t0 = tn;
-    t1 = tn + 1;
-    split = 0;
+    const int gm = (g.M + kBM - 1) / kBM;
+    int s;
+    grouped_map(bid, nb, gm, p.splits, tm, s);
+    split = s;
+    t0 = (int)(((long)p.tiles_n * s) / p.splits);
+    t1 = (int)(((long)p.tiles_n * (s + 1)) / p.splits);
   }
   static __device__ inline void init(State&) {}
   static __device__ inline void tile(const Params& p, State&, WaveAcc<BN, W>& acc, const GemmShape& g, int tm,
@@ -576,16 +622,16 @@ struct EpiAcc {
 // no prefetch registers are live while they run.
 // ---------------------------------------------------------------------------
 template <int BN, int W, bool AK, bool BKM, template <int, int> class EpiT, int PIPE>
-__global__ __launch_bounds__(W * 64) void gemm_kernel(GemmShape g, typename EpiT<BN, W>::Params ep) {
+__device__ __forceinline__ void gemm_body(const GemmShape& g, const typename EpiT<BN, W>::Params& ep, int bid,
+                                          int nb, bf16_t* smem) {
   typedef EpiT<BN, W> Epi;
   constexpr int kStage = (kBM + BN) * kPitch;
-  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * kStage];
 
   const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
   const int wm = w >> 1, wn = w & 1;
 
   int tm, t0, t1, split;
-  Epi::assign(g, ep, blockIdx.x, gridDim.x, tm, t0, t1, split);
+  Epi::assign(g, ep, bid, nb, tm, t0, t1, split);
   if (t0 >= t1) return;  // uniform for the whole workgroup
 
   typename Epi::State st;
@@ -597,6 +643,48 @@ __global__ __launch_bounds__(W * 64) void gemm_kernel(GemmShape g, typename EpiT
   const int a_r0 = tm * kBM;
   bf16_t* const S0 = smem;
   bf16_t* const S1 = smem + kStage;
+
+  if constexpr (PIPE == 4) {
+    // Direct-to-LDS pipeline: the DMA of slab s+1 is issued at the top of
+    // slab s into the idle stage; the barrier closing slab s (whose implied
+    // vmcnt(0) drains this wave's DMA) publishes it.  Both operands K-major,
+    // K a multiple of 64.
+    static_assert(AK && BKM, "direct-to-LDS loads need K-major operands");
+    constexpr int kSt = (kBM + BN) * 64;  // unpadded stage
+    bf16_t* const T0 = smem;
+    bf16_t* const T1 = smem + kSt;
+    dma_kmajor<kBM, W>(g.A, g.lda, a_r0, g.M, 0, T0, w, l);
+    dma_kmajor<BN, W>(g.B, g.ldb, t0 * BN, g.N, 0, T0 + kBM * 64, w, l);
+    __syncthreads();
+    int s = 0;
+    for (int tn = t0; tn < t1; ++tn) {
+      acc.zero();
+      for (int kt = 0; kt < KT; ++kt, ++s) {
+        bf16_t* const Sc = (s & 1) ? T1 : T0;
+        bf16_t* const Sn = (s & 1) ? T0 : T1;
+        const bool last_k = (kt + 1 == KT);
+        if (!(last_k && tn + 1 == t1)) {
+          const int nt = last_k ? tn + 1 : tn;
+          const int nk = last_k ? 0 : kt + 1;
+          dma_kmajor<kBM, W>(g.A, g.lda, a_r0, g.M, nk * kBK, Sn, w, l);
+          dma_kmajor<BN, W>(g.B, g.ldb, nt * BN, g.N, nk * kBK, Sn + kBM * 64, w, l);
+        }
+        Frags<BN, W> fa, fb;
+        read_frags_swz<BN, W>(Sc, Sc + kBM * 64, 0, fa, wm, wn, l);
+        read_frags_swz<BN, W>(Sc, Sc + kBM * 64, 1, fb, wm, wn, l);
+        mfma_frags<BN, W>(fa, acc);
+        read_frags_swz<BN, W>(Sc, Sc + kBM * 64, 2, fa, wm, wn, l);
+        mfma_frags<BN, W>(fb, acc);
+        read_frags_swz<BN, W>(Sc, Sc + kBM * 64, 3, fb, wm, wn, l);
+        mfma_frags<BN, W>(fa, acc);
+        mfma_frags<BN, W>(fb, acc);
+        __syncthreads();
+      }
+      Epi::tile(ep, st, acc, g, tm, tn, wm, wn, l);
+    }
+    Epi::finish(ep, st, g, tm, split, smem, wm, wn, l);
+    return;
+  }
 
   if constexpr (PIPE == 1) {
     // Simple pipeline: one slab in flight in registers, fragments read per
@@ -659,6 +747,11 @@ __global__ __launch_bounds__(W * 64) void gemm_kernel(GemmShape g, typename EpiT
     if constexpr (decltype(LOAD)::value) {
       la.load(g.A, g.lda, a_r0, g.M, nk * kBK, g.K, tid);
       lb.load(g.B, g.ldb, nt * BN, g.N, nk * kBK, g.K, tid);
+#ifdef CCE_PIN_LOADS
+      // keep the slab s+2 loads at the top of the slab: the scheduler would
+      // otherwise sink them below the LDS drain and halve the prefetch distance
+      __builtin_amdgcn_sched_barrier(0);
+#endif
     }
     read_frags<BN, W>(Sc, Sc + kBM * kPitch, 1, f1, wm, wn, l);
     mfma_frags<BN, W>(f0, acc);
@@ -708,6 +801,27 @@ __global__ __launch_bounds__(W * 64) void gemm_kernel(GemmShape g, typename EpiT
     Epi::tile(ep, st, acc, g, tm, tn, wm, wn, l);
   }
   Epi::finish(ep, st, g, tm, split, smem, wm, wn, l);
+}
+
+template <int BN, int W, bool AK, bool BKM, template <int, int> class EpiT, int PIPE>
+__global__ __launch_bounds__(W * 64) void gemm_kernel(GemmShape g, typename EpiT<BN, W>::Params ep) {
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * (kBM + BN) * kPitch];
+  gemm_body<BN, W, AK, BKM, EpiT, PIPE>(g, ep, blockIdx.x, gridDim.x, smem);
+}
+
+// dW and dH GEMMs of one vocabulary band in a single launch.  The first
+// nb_dw workgroups take dW tiles (K = N, the longer ones), the rest dH tiles
+// (K = band width), so the two tile populations pack the CUs together where
+// each alone would leave a partial last wave.
+template <int W, int BN_DW, int BN_DH, int PIPE_DH>
+__global__ __launch_bounds__(W * 64) void dual_acc_kernel(GemmShape g_dw, AccParams e_dw, int nb_dw, GemmShape g_dh,
+                                                          AccParams e_dh) {
+  constexpr int kMaxBN = BN_DW > BN_DH ? BN_DW : BN_DH;
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * (kBM + kMaxBN) * kPitch];
+  if ((int)blockIdx.x < nb_dw)
+    gemm_body<BN_DW, W, false, true, EpiAcc, 3>(g_dw, e_dw, blockIdx.x, nb_dw, smem);
+  else
+    gemm_body<BN_DH, W, true, true, EpiAcc, PIPE_DH>(g_dh, e_dh, blockIdx.x - nb_dw, gridDim.x - nb_dw, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -956,9 +1070,12 @@ struct Carver {
 
 // Forward vocabulary splits: enough (row tile x split) workgroups to cover
 // the 256 CUs several times over.
-int forward_splits(long N, long V) {
+bool fast_k(long K) { return K % 64 == 0; }
+int lse_bn(long d) { return fast_k(d) ? kFastBN : kSlowBN; }
+
+int forward_splits(long N, long d, long V) {
   if (N <= 0) return 1;
-  const long gm = ceil_div(N, kBM), tn = ceil_div(V, CCE_BN_LSE);
+  const long gm = ceil_div(N, kBM), tn = ceil_div(V, lse_bn(d));
   long s = ceil_div(2048, gm);
   if (s > tn) s = tn;
   if (s < 1) s = 1;
@@ -980,10 +1097,10 @@ struct FwdLayout {
   size_t bytes;
 };
 
-FwdLayout fwd_layout(void* ws, long N, long V, int reduction) {
+FwdLayout fwd_layout(void* ws, long N, long d, long V, int reduction) {
   Carver c(ws);
   FwdLayout L;
-  const int S = forward_splits(N, V);
+  const int S = forward_splits(N, d, V);
   const long nb = ceil_div(N, 4);
   L.pm = c.take<float>((size_t)S * N);
   L.ps = c.take<float>((size_t)S * N);
@@ -1089,10 +1206,26 @@ int zero_fill(void* p, size_t bytes, hipStream_t st) {
 }
 
 
-template <int BN, bool AK>
+int launch_dual_acc(const GemmShape& g_dw, const AccParams& e_dw, const GemmShape& g_dh, const AccParams& e_dh,
+                    hipStream_t st) {
+  // dH operands are K-major with K a multiple of 64 (the band is zero-padded)
+  constexpr int kBNdw = kSlowBN, kBNdh = kFastBN;
+  const int nb_dw = (int)(ceil_div(g_dw.M, kBM) * ceil_div(g_dw.N, kBNdw));
+  const int nb_dh = (int)(ceil_div(g_dh.M, kBM) * ceil_div(g_dh.N, kBNdh));
+  if (nb_dw + nb_dh <= 0) return CCE_OK;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  const bool timed = timing_begin(st, &t0, &t1);
+  hipLaunchKernelGGL((dual_acc_kernel<kWarp8, kBNdw, kBNdh, 4>), dim3(nb_dw + nb_dh), dim3(kWarp8 * 64), 0, st,
+                     g_dw, e_dw, nb_dw, g_dh, e_dh);
+  HIP_TRY(hipGetLastError());
+  if (timed) timing_end(CCE_KERNEL_BWD_DHDW, st, t0, t1);
+  return CCE_OK;
+}
+
+template <int BN, bool AK, int PIPE>
 int launch_acc(const GemmShape& g, const AccParams& ep, hipStream_t st, int kind) {
   const int nb = (int)(ceil_div(g.M, kBM) * ceil_div(g.N, BN));
-  return launch_gemm<BN, CCE_W_ACC, AK, true, EpiAcc>(g, ep, nb, st, kind);
+  return launch_gemm<BN, kWarp8, AK, true, EpiAcc, PIPE>(g, ep, nb, st, kind);
 }
 
 }  // namespace
@@ -1114,7 +1247,7 @@ int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, 
   if (rc) return rc;
   if (reduction < CCE_REDUCTION_NONE || reduction > CCE_REDUCTION_SUM)
     return fail(CCE_ERR_INVALID_ARG, "reduction must be 0 (none), 1 (mean) or 2 (sum), got %d", reduction);
-  *bytes = fwd_layout(nullptr, N, V, reduction).bytes;
+  *bytes = fwd_layout(nullptr, N, d, V, reduction).bytes;
   return CCE_OK;
 }
 
@@ -1146,7 +1279,7 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
   if (misaligned(hidden) || misaligned(weight) || misaligned(workspace))
     return fail(CCE_ERR_INVALID_ARG, "hidden, weight and workspace must be 16-byte aligned");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const FwdLayout need = fwd_layout(nullptr, N, V, reduction);
+  const FwdLayout need = fwd_layout(nullptr, N, d, V, reduction);
   if (workspace_bytes < need.bytes || (need.bytes && !workspace))
     return fail(CCE_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need.bytes, workspace_bytes);
   if (N == 0) {
@@ -1154,8 +1287,8 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
     if (!rc && reduction != CCE_REDUCTION_NONE) rc = zero_fill(loss_out, sizeof(float), st);
     return rc;
   }
-  const FwdLayout L = fwd_layout(workspace, N, V, reduction);
-  const int S = forward_splits(N, V);
+  const FwdLayout L = fwd_layout(workspace, N, d, V, reduction);
+  const int S = forward_splits(N, d, V);
   const int gm = (int)ceil_div(N, kBM);
 
   GemmShape g;
@@ -1171,11 +1304,13 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
   ep.pm = L.pm;
   ep.ps = L.ps;
   ep.splits = S;
-  ep.tiles_n = (int)ceil_div(V, CCE_BN_LSE);
-  rc = bias ? launch_gemm<CCE_BN_LSE, CCE_W_LSE, true, true, EpiLseBias, CCE_PIPE_LSE>(g, ep, gm * S, st,
-                                                                                      CCE_KERNEL_FWD_LSE)
-            : launch_gemm<CCE_BN_LSE, CCE_W_LSE, true, true, EpiLse, CCE_PIPE_LSE>(g, ep, gm * S, st,
-                                                                                  CCE_KERNEL_FWD_LSE);
+  ep.tiles_n = (int)ceil_div(V, lse_bn(d));
+  if (fast_k(d))
+    rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiLseBias, 4>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE)
+              : launch_gemm<kFastBN, kWarp8, true, true, EpiLse, 4>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE);
+  else
+    rc = bias ? launch_gemm<kSlowBN, kWarp8, true, true, EpiLseBias, 3>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE)
+              : launch_gemm<kSlowBN, kWarp8, true, true, EpiLse, 3>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE);
   if (rc) return rc;
 
   const int nb = (int)ceil_div(N, 4);
@@ -1256,34 +1391,35 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     g1.M = (int)N; g1.N = (int)vb; g1.K = (int)d;
     GradParams e1;
     e1.bias = bias; e1.rowp = L.rowp; e1.rowlab = L.rowlab; e1.G = L.G; e1.ldg = Vb; e1.v0 = (int)v0;
-    const int nb1 = gm * (int)ceil_div(vb, CCE_BN_GRAD);
-    rc = bias ? launch_gemm<CCE_BN_GRAD, CCE_W_GRAD, true, true, EpiGradBias, CCE_PIPE_GRAD>(g1, e1, nb1, st,
-                                                                                           CCE_KERNEL_BWD_GRAD)
-              : launch_gemm<CCE_BN_GRAD, CCE_W_GRAD, true, true, EpiGrad, CCE_PIPE_GRAD>(g1, e1, nb1, st,
-                                                                                       CCE_KERNEL_BWD_GRAD);
+    const int gbn = fast_k(d) ? kFastBN : kSlowBN;
+    e1.tiles_n = (int)ceil_div(vb, gbn);
+    e1.splits = (int)std::min<long>(e1.tiles_n, std::max<long>(1, ceil_div(CCE_GRAD_WGS, gm)));
+    const int nb1 = gm * e1.splits;
+    if (fast_k(d))
+      rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiGradBias, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD)
+                : launch_gemm<kFastBN, kWarp8, true, true, EpiGrad, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD);
+    else
+      rc = bias ? launch_gemm<kSlowBN, kWarp8, true, true, EpiGradBias, 3>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD)
+                : launch_gemm<kSlowBN, kWarp8, true, true, EpiGrad, 3>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD);
     if (rc) return rc;
 
+    GemmShape g2 = {}, g3 = {};
+    AccParams e2 = {}, e3 = {};
     if (need_dh) {
       // WT[j][c] = W[v0 + c][j], zero for vb <= c < vb64
       hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)ceil_div(vb64, 64), (unsigned)ceil_div(d, 64)), dim3(256),
                          0, st, W + v0 * d, (long)d, (int)vb, (int)d, L.WT, (long)Vb, (int)vb64);
       HIP_TRY(hipGetLastError());
-      GemmShape g2;
       g2.A = L.G; g2.lda = Vb; g2.B = L.WT; g2.ldb = Vb;
       g2.M = (int)N; g2.N = (int)d; g2.K = (int)vb64;
-      AccParams e2;
       e2.acc32 = L.dHacc; e2.ldacc = d; e2.out = grad_hidden; e2.ldo = d;
       e2.out_f32 = (grad_hidden_dtype == CCE_DTYPE_F32);
       e2.mode = (nbands == 1) ? 0 : (b == 0 ? 1 : (b == nbands - 1 ? 3 : 2));
-      rc = launch_acc<128, true>(g2, e2, st, CCE_KERNEL_BWD_DH);
-      if (rc) return rc;
     }
     if (need_dw) {
-      GemmShape g3;
       g3.A = L.G; g3.lda = Vb;  // MN-major: element (v, n) at G[n*Vb + v]
       g3.B = L.HT; g3.ldb = N8;
       g3.M = (int)vb; g3.N = (int)d; g3.K = (int)N;
-      AccParams e3;
       e3.acc32 = nullptr; e3.ldacc = 0;
       e3.out = (grad_weight_dtype == CCE_DTYPE_F32)
                    ? static_cast<void*>(static_cast<float*>(grad_weight) + v0 * d)
@@ -1291,9 +1427,14 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       e3.ldo = d;
       e3.out_f32 = (grad_weight_dtype == CCE_DTYPE_F32);
       e3.mode = 0;
-      rc = launch_acc<128, false>(g3, e3, st, CCE_KERNEL_BWD_DW);
-      if (rc) return rc;
     }
+    if (need_dh && need_dw)
+      rc = launch_dual_acc(g3, e3, g2, e2, st);
+    else if (need_dh)
+      rc = launch_acc<kFastBN, true, 4>(g2, e2, st, CCE_KERNEL_BWD_DH);
+    else if (need_dw)
+      rc = launch_acc<kSlowBN, false, 3>(g3, e3, st, CCE_KERNEL_BWD_DW);
+    if (rc) return rc;
     if (need_db) {
       hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)ceil_div(vb, 64)), dim3(256), 0, st, L.G, (long)Vb, (int)N,
                          (int)vb, grad_bias + v0);

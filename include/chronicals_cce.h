@@ -117,7 +117,8 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
 #define CCE_KERNEL_BWD_GRAD 1  /* backward recompute GEMM -> dLoss/dS     */
 #define CCE_KERNEL_BWD_DH 2    /* dHidden GEMM (per vocabulary band)      */
 #define CCE_KERNEL_BWD_DW 3    /* dWeight GEMM (per vocabulary band)      */
-#define CCE_KERNEL_KINDS 4
+#define CCE_KERNEL_BWD_DHDW 4  /* dHidden + dWeight GEMMs in one launch   */
+#define CCE_KERNEL_KINDS 5
 int cce_kernel_timing_enable(int enable);
 int cce_kernel_timing_read(int kind, double* total_ms, int64_t* launches);
 
