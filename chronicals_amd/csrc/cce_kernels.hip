@@ -291,6 +291,43 @@ __device__ inline void dma_kmajor(const bf16_t* __restrict__ X, long ld, int r0,
   }
 }
 
+// MN-major tile for PIPE 5: element (m, k) at X[k*ld + m].  The tile
+// k [k0, k0 + 64) x m [m0, m0 + 256) is copied in its natural [k][m] layout
+// (512 B per k row; one wave instruction = 2 rows), with 16-byte chunk c of
+// row k stored at physical chunk c ^ (4*(k & 3)) so the four rows touched by
+// one transposed fragment read land on distinct banks.  Rows k >= K fall
+// outside the descriptor's range and read as zero.
+template <int W>
+__device__ inline void dma_mnmajor256(const bf16_t* __restrict__ X, long ld, int m0, int k0, int K, bf16_t* S,
+                                      int w, int l) {
+  constexpr int kI = 32 / W;  // 32 wave instructions per 64 x 256 tile
+  const long rows_left = (long)K - k0;
+  const long bytes = rows_left > 0 ? (rows_left * ld - m0) * 2 : 0;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(X + (long)k0 * ld + m0, bytes);
+#pragma unroll
+  for (int j = 0; j < kI; ++j) {
+    const int blk = w * kI + j;  // pair of k rows
+    const int row = blk * 2 + (l >> 5);
+    const int c = (l & 31) ^ (4 * (row & 3));
+    const int voff = (int)(((long)row * ld + c * 8) * 2);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rs, (__attribute__((address_space(3))) void*)(S + blk * 512), 16, voff, 0, 0, 0);
+  }
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// ds_read_b64_tr_b16: in each 16-lane group, lane j receives element j&3 of
+// the 8-byte reads addressed by lanes (j>>2) + 4t, t = 0..3.  Lane a of the
+// group addresses row k = kb + (a>>2), columns m = mb + 4*(a&3) .. +3 of the
+// [k][m] tile, so lane j receives k = kb..kb+3 of column m = mb + j.
+__device__ inline uint2 read_tr4(const bf16_t* S, int k, int m) {
+  const int phys = (((m >> 3) ^ (4 * (k & 3))) << 3) + (m & 7);
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(S + k * 256 + phys));
+  return __builtin_bit_cast(uint2, v);
+}
+
 // Register fragments of one k-step (16 of K) for a wave.
 template <int BN, int W>
 struct Frags {
@@ -319,6 +356,29 @@ __device__ inline void read_frags_swz(const bf16_t* __restrict__ As, const bf16_
     const int r = wm * WaveCfg<W>::kWaveRows + i * 32 + (l & 31);
     f.a[i] = *reinterpret_cast<const u32x4*>(As + r * 64 + ((c ^ swz(r)) << 3));
   }
+#pragma unroll
+  for (int j = 0; j < BN / 64; ++j) {
+    const int r = wn * (BN / 2) + j * 32 + (l & 31);
+    f.b[j] = *reinterpret_cast<const u32x4*>(Bs + r * 64 + ((c ^ swz(r)) << 3));
+  }
+}
+
+// A fragments from the [k][m] tile with transposed reads (PIPE 5): lane l
+// gets m = i*32 + (l & 31), k = kk*16 + 8*(l >> 5) + 0..7 — the same k map as
+// the K-major B fragments.
+template <int BN, int W>
+__device__ inline void read_frags_tr(const bf16_t* __restrict__ As, const bf16_t* __restrict__ Bs, int kk,
+                                     Frags<BN, W>& f, int wm, int wn, int l) {
+  const int a = l & 15;
+  const int kb = kk * 16 + 8 * (l >> 5) + (a >> 2);
+#pragma unroll
+  for (int i = 0; i < WaveCfg<W>::kFM; ++i) {
+    const int mb = wm * WaveCfg<W>::kWaveRows + i * 32 + 16 * ((l >> 4) & 1) + 4 * (a & 3);
+    const uint2 lo = read_tr4(As, kb, mb);
+    const uint2 hi = read_tr4(As, kb + 4, mb);
+    f.a[i] = u32x4{lo.x, lo.y, hi.x, hi.y};
+  }
+  const int c = kk * 2 + (l >> 5);
 #pragma unroll
   for (int j = 0; j < BN / 64; ++j) {
     const int r = wn * (BN / 2) + j * 32 + (l & 31);
@@ -644,16 +704,30 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
   bf16_t* const S0 = smem;
   bf16_t* const S1 = smem + kStage;
 
-  if constexpr (PIPE == 4) {
+  if constexpr (PIPE == 4 || PIPE == 5) {
     // Direct-to-LDS pipeline: the DMA of slab s+1 is issued at the top of
     // slab s into the idle stage; the barrier closing slab s (whose implied
-    // vmcnt(0) drains this wave's DMA) publishes it.  Both operands K-major,
-    // K a multiple of 64.
-    static_assert(AK && BKM, "direct-to-LDS loads need K-major operands");
+    // vmcnt(0) drains this wave's DMA) publishes it.  B is K-major; A is
+    // K-major (PIPE 4) or MN-major read back transposed (PIPE 5).  K-major
+    // operands need K a multiple of 64 (or zero padding up to one).
+    static_assert(BKM && (PIPE == 5 || AK), "direct-to-LDS operand layouts");
+    static_assert(PIPE == 4 || (!AK && BN <= 256), "PIPE 5 reads an MN-major A");
     constexpr int kSt = (kBM + BN) * 64;  // unpadded stage
     bf16_t* const T0 = smem;
     bf16_t* const T1 = smem + kSt;
-    dma_kmajor<kBM, W>(g.A, g.lda, a_r0, g.M, 0, T0, w, l);
+    auto dma_a = [&](int k0, bf16_t* S) {
+      if constexpr (PIPE == 4)
+        dma_kmajor<kBM, W>(g.A, g.lda, a_r0, g.M, k0, S, w, l);
+      else
+        dma_mnmajor256<W>(g.A, g.lda, a_r0, k0, g.K, S, w, l);
+    };
+    auto frags = [&](const bf16_t* Sc, int kk, Frags<BN, W>& f) {
+      if constexpr (PIPE == 4)
+        read_frags_swz<BN, W>(Sc, Sc + kBM * 64, kk, f, wm, wn, l);
+      else
+        read_frags_tr<BN, W>(Sc, Sc + kBM * 64, kk, f, wm, wn, l);
+    };
+    dma_a(0, T0);
     dma_kmajor<BN, W>(g.B, g.ldb, t0 * BN, g.N, 0, T0 + kBM * 64, w, l);
     __syncthreads();
     int s = 0;
@@ -666,16 +740,16 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
         if (!(last_k && tn + 1 == t1)) {
           const int nt = last_k ? tn + 1 : tn;
           const int nk = last_k ? 0 : kt + 1;
-          dma_kmajor<kBM, W>(g.A, g.lda, a_r0, g.M, nk * kBK, Sn, w, l);
+          dma_a(nk * kBK, Sn);
           dma_kmajor<BN, W>(g.B, g.ldb, nt * BN, g.N, nk * kBK, Sn + kBM * 64, w, l);
         }
         Frags<BN, W> fa, fb;
-        read_frags_swz<BN, W>(Sc, Sc + kBM * 64, 0, fa, wm, wn, l);
-        read_frags_swz<BN, W>(Sc, Sc + kBM * 64, 1, fb, wm, wn, l);
+        frags(Sc, 0, fa);
+        frags(Sc, 1, fb);
         mfma_frags<BN, W>(fa, acc);
-        read_frags_swz<BN, W>(Sc, Sc + kBM * 64, 2, fa, wm, wn, l);
+        frags(Sc, 2, fa);
         mfma_frags<BN, W>(fb, acc);
-        read_frags_swz<BN, W>(Sc, Sc + kBM * 64, 3, fb, wm, wn, l);
+        frags(Sc, 3, fb);
         mfma_frags<BN, W>(fa, acc);
         mfma_frags<BN, W>(fb, acc);
         __syncthreads();
@@ -813,13 +887,13 @@ __global__ __launch_bounds__(W * 64) void gemm_kernel(GemmShape g, typename EpiT
 // nb_dw workgroups take dW tiles (K = N, the longer ones), the rest dH tiles
 // (K = band width), so the two tile populations pack the CUs together where
 // each alone would leave a partial last wave.
-template <int W, int BN_DW, int BN_DH, int PIPE_DH>
+template <int W, int BN_DW, int PIPE_DW, int BN_DH, int PIPE_DH>
 __global__ __launch_bounds__(W * 64) void dual_acc_kernel(GemmShape g_dw, AccParams e_dw, int nb_dw, GemmShape g_dh,
                                                           AccParams e_dh) {
   constexpr int kMaxBN = BN_DW > BN_DH ? BN_DW : BN_DH;
   __shared__ __attribute__((aligned(16))) bf16_t smem[2 * (kBM + kMaxBN) * kPitch];
   if ((int)blockIdx.x < nb_dw)
-    gemm_body<BN_DW, W, false, true, EpiAcc, 3>(g_dw, e_dw, blockIdx.x, nb_dw, smem);
+    gemm_body<BN_DW, W, false, true, EpiAcc, PIPE_DW>(g_dw, e_dw, blockIdx.x, nb_dw, smem);
   else
     gemm_body<BN_DH, W, true, true, EpiAcc, PIPE_DH>(g_dh, e_dh, blockIdx.x - nb_dw, gridDim.x - nb_dw, smem);
 }
@@ -1208,14 +1282,15 @@ int zero_fill(void* p, size_t bytes, hipStream_t st) {
 
 int launch_dual_acc(const GemmShape& g_dw, const AccParams& e_dw, const GemmShape& g_dh, const AccParams& e_dh,
                     hipStream_t st) {
-  // dH operands are K-major with K a multiple of 64 (the band is zero-padded)
+  // dH operands are K-major with K a multiple of 64 (the band is zero-padded);
+  // dW reads G transposed from LDS (its K tail reads as zero past row N)
   constexpr int kBNdw = kSlowBN, kBNdh = kFastBN;
   const int nb_dw = (int)(ceil_div(g_dw.M, kBM) * ceil_div(g_dw.N, kBNdw));
   const int nb_dh = (int)(ceil_div(g_dh.M, kBM) * ceil_div(g_dh.N, kBNdh));
   if (nb_dw + nb_dh <= 0) return CCE_OK;
   hipEvent_t t0 = nullptr, t1 = nullptr;
   const bool timed = timing_begin(st, &t0, &t1);
-  hipLaunchKernelGGL((dual_acc_kernel<kWarp8, kBNdw, kBNdh, 4>), dim3(nb_dw + nb_dh), dim3(kWarp8 * 64), 0, st,
+  hipLaunchKernelGGL((dual_acc_kernel<kWarp8, kBNdw, 5, kBNdh, 4>), dim3(nb_dw + nb_dh), dim3(kWarp8 * 64), 0, st,
                      g_dw, e_dw, nb_dw, g_dh, e_dh);
   HIP_TRY(hipGetLastError());
   if (timed) timing_end(CCE_KERNEL_BWD_DHDW, st, t0, t1);
@@ -1433,7 +1508,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     else if (need_dh)
       rc = launch_acc<kFastBN, true, 4>(g2, e2, st, CCE_KERNEL_BWD_DH);
     else if (need_dw)
-      rc = launch_acc<kSlowBN, false, 3>(g3, e3, st, CCE_KERNEL_BWD_DW);
+      rc = launch_acc<kSlowBN, false, 5>(g3, e3, st, CCE_KERNEL_BWD_DW);
     if (rc) return rc;
     if (need_db) {
       hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)ceil_div(vb, 64)), dim3(256), 0, st, L.G, (long)Vb, (int)N,
