@@ -705,54 +705,86 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
   bf16_t* const S1 = smem + kStage;
 
   if constexpr (PIPE == 4 || PIPE == 5) {
-    // Direct-to-LDS pipeline: the DMA of slab s+1 is issued at the top of
-    // slab s into the idle stage; the barrier closing slab s (whose implied
-    // vmcnt(0) drains this wave's DMA) publishes it.  B is K-major; A is
-    // K-major (PIPE 4) or MN-major read back transposed (PIPE 5).  K-major
-    // operands need K a multiple of 64 (or zero padding up to one).
+    // Direct-to-LDS pipeline over the workgroup's slabs s = 0, 1, ... (a run
+    // of column tiles times KT slabs each), LDS stage s & 1.  Per slab:
+    //   k-steps 0..2: MFMAs, with the fragments of the next k-step read
+    //                 from LDS behind them;
+    //   barrier B_s:  its implied vmcnt(0) / lgkmcnt(0) mean slab s+1's DMA
+    //                 (issued after B_{s-1}) has landed for every wave and no
+    //                 wave still reads slab s's stage;
+    //   then the DMA of slab s+2 into that stage and the first fragments of
+    //   slab s+1 are issued while the MFMAs of k-step 3 (whose fragments are
+    //   already in registers) run, so the barrier's read bubble is hidden.
+    // B is K-major; A is K-major (PIPE 4) or MN-major read back transposed
+    // (PIPE 5).  K-major operands need K a multiple of 64 (or zero padding).
     static_assert(BKM && (PIPE == 5 || AK), "direct-to-LDS operand layouts");
     static_assert(PIPE == 4 || (!AK && BN <= 256), "PIPE 5 reads an MN-major A");
     constexpr int kSt = (kBM + BN) * 64;  // unpadded stage
     bf16_t* const T0 = smem;
     bf16_t* const T1 = smem + kSt;
-    auto dma_a = [&](int k0, bf16_t* S) {
-      if constexpr (PIPE == 4)
-        dma_kmajor<kBM, W>(g.A, g.lda, a_r0, g.M, k0, S, w, l);
-      else
-        dma_mnmajor256<W>(g.A, g.lda, a_r0, k0, g.K, S, w, l);
-    };
     auto frags = [&](const bf16_t* Sc, int kk, Frags<BN, W>& f) {
       if constexpr (PIPE == 4)
         read_frags_swz<BN, W>(Sc, Sc + kBM * 64, kk, f, wm, wn, l);
       else
         read_frags_tr<BN, W>(Sc, Sc + kBM * 64, kk, f, wm, wn, l);
     };
-    dma_a(0, T0);
-    dma_kmajor<BN, W>(g.B, g.ldb, t0 * BN, g.N, 0, T0 + kBM * 64, w, l);
-    __syncthreads();
+    // DMA of the next unissued slab (tile it2, k-slab ik2) into stage S
+    int it2 = t0, ik2 = 0;
+    auto issue = [&](bf16_t* S) {
+      if constexpr (PIPE == 4)
+        dma_kmajor<kBM, W>(g.A, g.lda, a_r0, g.M, ik2 * kBK, S, w, l);
+      else
+        dma_mnmajor256<W>(g.A, g.lda, a_r0, ik2 * kBK, g.K, S, w, l);
+      dma_kmajor<BN, W>(g.B, g.ldb, it2 * BN, g.N, ik2 * kBK, S + kBM * 64, w, l);
+      if (++ik2 == KT) {
+        ik2 = 0;
+        ++it2;
+      }
+    };
+    // The DMA's LDS writes count on vmcnt; the barrier's own fence does not
+    // reliably wait for them, so each barrier that publishes a slab is
+    // preceded by an explicit vmcnt(0).  sched_barrier fences keep the MFMAs
+    // on their side of it.
+    auto publish = [&]() {
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    // each k-step: the next k-step's fragment reads are issued first, then
+    // the MFMAs they hide behind
+    auto order = [&]() {
+      constexpr int kReads = (PIPE == 4 ? 1 : 2) * WaveCfg<W>::kFM + BN / 64;
+      __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, WaveCfg<W>::kFM * (BN / 64), 0);
+    };
+    const int total = (t1 - t0) * KT;
+    issue(T0);
+    if (total > 1) issue(T1);
+    publish();
+    Frags<BN, W> fa, fb;
+    frags(T0, 0, fa);
     int s = 0;
     for (int tn = t0; tn < t1; ++tn) {
       acc.zero();
       for (int kt = 0; kt < KT; ++kt, ++s) {
         bf16_t* const Sc = (s & 1) ? T1 : T0;
         bf16_t* const Sn = (s & 1) ? T0 : T1;
-        const bool last_k = (kt + 1 == KT);
-        if (!(last_k && tn + 1 == t1)) {
-          const int nt = last_k ? tn + 1 : tn;
-          const int nk = last_k ? 0 : kt + 1;
-          dma_a(nk * kBK, Sn);
-          dma_kmajor<BN, W>(g.B, g.ldb, nt * BN, g.N, nk * kBK, Sn + kBM * 64, w, l);
-        }
-        Frags<BN, W> fa, fb;
-        frags(Sc, 0, fa);
         frags(Sc, 1, fb);
         mfma_frags<BN, W>(fa, acc);
+        order();
         frags(Sc, 2, fa);
         mfma_frags<BN, W>(fb, acc);
+        order();
         frags(Sc, 3, fb);
         mfma_frags<BN, W>(fa, acc);
+        order();
+        publish();         // B_s
+        frags(Sn, 0, fa);  // past the last slab this reads stale data, unused
         mfma_frags<BN, W>(fb, acc);
-        __syncthreads();
+        order();
+        __builtin_amdgcn_sched_barrier(0);
+        if (s + 2 < total) issue(Sc);
       }
       Epi::tile(ep, st, acc, g, tm, tn, wm, wn, l);
     }
