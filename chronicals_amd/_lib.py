@@ -11,7 +11,7 @@ import threading
 from . import build as _build
 
 # constants mirrored from include/chronicals_cce.h
-CCE_ABI_VERSION = 1
+CCE_ABI_VERSION = 2
 CCE_OK = 0
 CCE_ERR_INVALID_ARG = 1
 CCE_ERR_WORKSPACE = 2
@@ -27,9 +27,10 @@ CCE_KERNEL_BWD_GRAD = 1
 CCE_KERNEL_BWD_DH = 2
 CCE_KERNEL_BWD_DW = 3
 CCE_KERNEL_BWD_DHDW = 4
-CCE_KERNEL_KINDS = 5
+CCE_KERNEL_BWD_BAND = 5
+CCE_KERNEL_KINDS = 6
 KERNEL_KIND_NAMES = {CCE_KERNEL_FWD_LSE: "fwd_lse", CCE_KERNEL_BWD_GRAD: "bwd_grad", CCE_KERNEL_BWD_DH: "bwd_dh",
-                     CCE_KERNEL_BWD_DW: "bwd_dw", CCE_KERNEL_BWD_DHDW: "bwd_dhdw"}
+                     CCE_KERNEL_BWD_DW: "bwd_dw", CCE_KERNEL_BWD_DHDW: "bwd_dhdw", CCE_KERNEL_BWD_BAND: "bwd_band"}
 
 REDUCTIONS = {"none": CCE_REDUCTION_NONE, "mean": CCE_REDUCTION_MEAN, "sum": CCE_REDUCTION_SUM}
 
@@ -61,7 +62,8 @@ SIGNATURES = {
         _vp, _sz, _vp,                       # workspace, workspace_bytes, stream
     ]),
     "cce_kernel_timing_enable": (_i32, [_i32]),
-    "cce_kernel_timing_read": (_i32, [_i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64)]),
+    "cce_kernel_timing_read": (_i32, [_i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64),
+                                      ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
 }
 
 _lock = threading.Lock()
@@ -125,8 +127,11 @@ def kernel_timing_enable(enable: bool) -> None:
 
 
 def kernel_timing_read(kind: int):
-    """(total milliseconds, launches) recorded for one kernel kind since the last read."""
+    """(total milliseconds, launches, credited FLOPs, executed FLOPs) recorded for one
+    kernel kind since the last read."""
     ms = ctypes.c_double(0.0)
     n = _i64(0)
-    check(load().cce_kernel_timing_read(kind, ctypes.byref(ms), ctypes.byref(n)))
-    return ms.value, n.value
+    cr = ctypes.c_double(0.0)
+    ex = ctypes.c_double(0.0)
+    check(load().cce_kernel_timing_read(kind, ctypes.byref(ms), ctypes.byref(n), ctypes.byref(cr), ctypes.byref(ex)))
+    return ms.value, n.value, cr.value, ex.value

@@ -930,6 +930,50 @@ __global__ __launch_bounds__(W * 64) void dual_acc_kernel(GemmShape g_dw, AccPar
     gemm_body<BN_DH, W, true, true, EpiAcc, PIPE_DH>(g_dh, e_dh, blockIdx.x - nb_dw, gridDim.x - nb_dw, smem);
 }
 
+// One launch per vocabulary band b of the backward (d a multiple of 64): the
+// dW and dH GEMMs of band b and the logits recompute of band b+1, which
+// writes the other G buffer.  Workgroups are numbered longest first — dW
+// (K = N), dH (K = band width; d in 256-wide column tiles plus one 128-wide
+// tail tile when d % 256 <= 128, so no MFMA work is spent on padding), then
+// the short recompute tiles — so the recompute fills the CUs the long tiles
+// leave idle at the end of the band.
+struct BandLaunch {
+  GemmShape dw;
+  AccParams e_dw;
+  GemmShape dh;
+  AccParams e_dh;
+  GemmShape dh2;
+  AccParams e_dh2;
+  GemmShape gr;
+  GradParams e_gr;
+  int nb_dw, nb_dh, nb_dh2, nb_gr;
+};
+
+template <bool HB>
+__global__ __launch_bounds__(kWarp8 * 64) void band_kernel(BandLaunch p) {
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * (kBM + kFastBN) * 64];
+  int b = blockIdx.x;
+  if (b < p.nb_dw) {
+    gemm_body<kSlowBN, kWarp8, false, true, EpiAcc, 5>(p.dw, p.e_dw, b, p.nb_dw, smem);
+    return;
+  }
+  b -= p.nb_dw;
+  if (b < p.nb_dh) {
+    gemm_body<kFastBN, kWarp8, true, true, EpiAcc, 4>(p.dh, p.e_dh, b, p.nb_dh, smem);
+    return;
+  }
+  b -= p.nb_dh;
+  if (b < p.nb_dh2) {
+    gemm_body<kSlowBN, kWarp8, true, true, EpiAcc, 4>(p.dh2, p.e_dh2, b, p.nb_dh2, smem);
+    return;
+  }
+  b -= p.nb_dh2;
+  if constexpr (HB)
+    gemm_body<kFastBN, kWarp8, true, true, EpiGradBias, 4>(p.gr, p.e_gr, b, p.nb_gr, smem);
+  else
+    gemm_body<kFastBN, kWarp8, true, true, EpiGrad, 4>(p.gr, p.e_gr, b, p.nb_gr, smem);
+}
+
 // ---------------------------------------------------------------------------
 // Auxiliary kernels
 // ---------------------------------------------------------------------------
@@ -1220,12 +1264,16 @@ FwdLayout fwd_layout(void* ws, long N, long d, long V, int reduction) {
 struct BwdLayout {
   float4* rowp;
   int* rowlab;
-  bf16_t* G;
+  bf16_t* G[2];  // band gradient buffers; the second only when bands alternate
   bf16_t* WT;
   bf16_t* HT;
   float* dHacc;
   size_t bytes;
 };
+
+// The banded backward with the band kernel (d a multiple of 64) overlaps the
+// recompute of band b+1 with the dW / dH GEMMs of band b: two G buffers.
+bool banded(long d) { return d % 64 == 0; }
 
 BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bool need_dw) {
   Carver c(ws);
@@ -1234,7 +1282,8 @@ BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bo
   const long N8 = (long)align_up((size_t)N, 8);
   L.rowp = c.take<float4>((size_t)N);
   L.rowlab = c.take<int>((size_t)N);
-  L.G = c.take<bf16_t>((size_t)N * Vb);
+  L.G[0] = c.take<bf16_t>((size_t)N * Vb);
+  L.G[1] = (banded(d) && nbands > 1) ? c.take<bf16_t>((size_t)N * Vb) : L.G[0];
   L.WT = need_dh ? c.take<bf16_t>((size_t)d * Vb) : nullptr;
   L.HT = need_dw ? c.take<bf16_t>((size_t)d * N8) : nullptr;
   L.dHacc = (need_dh && nbands > 1) ? c.take<float>((size_t)N * d) : nullptr;
@@ -1254,10 +1303,14 @@ int check_dims(long N, long d, long V) {
 }
 
 // Optional per-kind kernel timing (cce_kernel_timing_enable).
+struct TimedLaunch {
+  hipEvent_t ev0, ev1;
+  double credited, executed;  // algorithmic / executed MFMA FLOPs of the launch
+};
 struct KernelTiming {
   std::mutex mu;
   bool enabled = false;
-  std::vector<std::pair<hipEvent_t, hipEvent_t>> pending[CCE_KERNEL_KINDS];
+  std::vector<TimedLaunch> pending[CCE_KERNEL_KINDS];
   std::vector<hipEvent_t> pool;
   hipEvent_t get() {
     if (!pool.empty()) {
@@ -1282,20 +1335,28 @@ bool timing_begin(hipStream_t st, hipEvent_t* ev0, hipEvent_t* ev1) {
   return hipEventRecord(*ev0, st) == hipSuccess;
 }
 
-void timing_end(int kind, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+void timing_end(int kind, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1, double credited, double executed) {
   std::lock_guard<std::mutex> lk(g_timing.mu);
-  if (hipEventRecord(ev1, st) == hipSuccess) g_timing.pending[kind].emplace_back(ev0, ev1);
+  if (hipEventRecord(ev1, st) == hipSuccess) g_timing.pending[kind].push_back({ev0, ev1, credited, executed});
 }
 
+// MFMA FLOPs of an M x N x K GEMM
+double gemm_flops(long M, long N, long K) { return 2.0 * (double)M * (double)N * (double)K; }
+
+// A GEMM launch; `credited` is the algorithmic share of its FLOPs (the
+// logits recompute of the backward is executed but not credited).
 template <int BN, int W, bool AK, bool BK, template <int, int> class EpiT, int PIPE = 3>
 int launch_gemm(const GemmShape& g, const typename EpiT<BN, W>::Params& ep, int nblocks, hipStream_t st,
-                int kind) {
+                int kind, bool credited) {
   if (nblocks <= 0) return CCE_OK;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   const bool timed = timing_begin(st, &e0, &e1);
   hipLaunchKernelGGL((gemm_kernel<BN, W, AK, BK, EpiT, PIPE>), dim3(nblocks), dim3(W * 64), 0, st, g, ep);
   HIP_TRY(hipGetLastError());
-  if (timed) timing_end(kind, st, e0, e1);
+  if (timed) {
+    const double f = gemm_flops(g.M, g.N, g.K);
+    timing_end(kind, st, e0, e1, credited ? f : 0.0, f);
+  }
   return CCE_OK;
 }
 
@@ -1325,14 +1386,50 @@ int launch_dual_acc(const GemmShape& g_dw, const AccParams& e_dw, const GemmShap
   hipLaunchKernelGGL((dual_acc_kernel<kWarp8, kBNdw, 5, kBNdh, 4>), dim3(nb_dw + nb_dh), dim3(kWarp8 * 64), 0, st,
                      g_dw, e_dw, nb_dw, g_dh, e_dh);
   HIP_TRY(hipGetLastError());
-  if (timed) timing_end(CCE_KERNEL_BWD_DHDW, st, t0, t1);
+  if (timed) {
+    const double f = gemm_flops(g_dw.M, g_dw.N, g_dw.K) + gemm_flops(g_dh.M, g_dh.N, g_dh.K);
+    timing_end(CCE_KERNEL_BWD_DHDW, st, t0, t1, f, f);
+  }
   return CCE_OK;
 }
 
 template <int BN, bool AK, int PIPE>
 int launch_acc(const GemmShape& g, const AccParams& ep, hipStream_t st, int kind) {
   const int nb = (int)(ceil_div(g.M, kBM) * ceil_div(g.N, BN));
-  return launch_gemm<BN, kWarp8, AK, true, EpiAcc, PIPE>(g, ep, nb, st, kind);
+  return launch_gemm<BN, kWarp8, AK, true, EpiAcc, PIPE>(g, ep, nb, st, kind, true);
+}
+
+// Recompute launch shape of one band: G[n][c] for columns [v0, v0 + vb).
+void grad_shape(const bf16_t* H, const bf16_t* W, const float* bias, const BwdLayout& L, bf16_t* G, long N, long d,
+                long Vb, long v0, long vb, int bn, GemmShape& g, GradParams& e, int& nb) {
+  const int gm = (int)ceil_div(N, kBM);
+  g.A = H; g.lda = d; g.B = W + v0 * d; g.ldb = d;
+  g.M = (int)N; g.N = (int)vb; g.K = (int)d;
+  e.bias = bias; e.rowp = L.rowp; e.rowlab = L.rowlab; e.G = G; e.ldg = Vb; e.v0 = (int)v0;
+  e.tiles_n = (int)ceil_div(vb, bn);
+  e.splits = (int)std::min<long>(e.tiles_n, std::max<long>(1, ceil_div(CCE_GRAD_WGS, gm)));
+  nb = gm * e.splits;
+}
+
+int launch_band(const BandLaunch& p, bool has_bias, hipStream_t st) {
+  const int nb = p.nb_dw + p.nb_dh + p.nb_dh2 + p.nb_gr;
+  if (nb <= 0) return CCE_OK;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  const bool timed = timing_begin(st, &t0, &t1);
+  if (has_bias)
+    hipLaunchKernelGGL(band_kernel<true>, dim3(nb), dim3(kWarp8 * 64), 0, st, p);
+  else
+    hipLaunchKernelGGL(band_kernel<false>, dim3(nb), dim3(kWarp8 * 64), 0, st, p);
+  HIP_TRY(hipGetLastError());
+  if (timed) {
+    double cr = 0.0;
+    if (p.nb_dw) cr += gemm_flops(p.dw.M, p.dw.N, p.dw.K);
+    if (p.nb_dh) cr += gemm_flops(p.dh.M, p.dh.N, p.dh.K);
+    if (p.nb_dh2) cr += gemm_flops(p.dh2.M, p.dh2.N, p.dh2.K);
+    const double ex = cr + (p.nb_gr ? gemm_flops(p.gr.M, p.gr.N, p.gr.K) : 0.0);
+    timing_end(CCE_KERNEL_BWD_BAND, st, t0, t1, cr, ex);
+  }
+  return CCE_OK;
 }
 
 }  // namespace
@@ -1413,11 +1510,11 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
   ep.splits = S;
   ep.tiles_n = (int)ceil_div(V, lse_bn(d));
   if (fast_k(d))
-    rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiLseBias, 4>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE)
-              : launch_gemm<kFastBN, kWarp8, true, true, EpiLse, 4>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE);
+    rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiLseBias, 4>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE, true)
+              : launch_gemm<kFastBN, kWarp8, true, true, EpiLse, 4>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE, true);
   else
-    rc = bias ? launch_gemm<kSlowBN, kWarp8, true, true, EpiLseBias, 3>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE)
-              : launch_gemm<kSlowBN, kWarp8, true, true, EpiLse, 3>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE);
+    rc = bias ? launch_gemm<kSlowBN, kWarp8, true, true, EpiLseBias, 3>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE, true)
+              : launch_gemm<kSlowBN, kWarp8, true, true, EpiLse, 3>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE, true);
   if (rc) return rc;
 
   const int nb = (int)ceil_div(N, 4);
@@ -1487,54 +1584,125 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
 
   const long nbands = ceil_div(V, Vb);
   const int gm = (int)ceil_div(N, kBM);
+  auto band_cols = [&](long b, long& v0, long& vb, long& vb64) {
+    v0 = b * Vb;
+    vb = (V - v0 < Vb) ? (V - v0) : Vb;
+    vb64 = (long)align_up((size_t)vb, 64);
+  };
+  // dH of one band: G[N][vb64] . WT[d][vb64]^T over hidden columns [c0, c0 + nc)
+  auto dh_shape = [&](long b, const bf16_t* G, long c0, long nc, GemmShape& g, AccParams& e) {
+    long v0, vb, vb64;
+    band_cols(b, v0, vb, vb64);
+    g.A = G; g.lda = Vb; g.B = L.WT + c0 * Vb; g.ldb = Vb;
+    g.M = (int)N; g.N = (int)nc; g.K = (int)vb64;
+    e.acc32 = L.dHacc ? L.dHacc + c0 : nullptr; e.ldacc = d;
+    e.out = (grad_hidden_dtype == CCE_DTYPE_F32) ? static_cast<void*>(static_cast<float*>(grad_hidden) + c0)
+                                                 : static_cast<void*>(static_cast<bf16_t*>(grad_hidden) + c0);
+    e.ldo = d;
+    e.out_f32 = (grad_hidden_dtype == CCE_DTYPE_F32);
+    e.mode = (nbands == 1) ? 0 : (b == 0 ? 1 : (b == nbands - 1 ? 3 : 2));
+  };
+  // dW of one band: rows [v0, v0 + vb) of grad_weight = G^T . H
+  auto dw_shape = [&](long b, const bf16_t* G, GemmShape& g, AccParams& e) {
+    long v0, vb, vb64;
+    band_cols(b, v0, vb, vb64);
+    g.A = G; g.lda = Vb;  // MN-major: element (v, n) at G[n*Vb + v]
+    g.B = L.HT; g.ldb = N8;
+    g.M = (int)vb; g.N = (int)d; g.K = (int)N;
+    e.acc32 = nullptr; e.ldacc = 0;
+    e.out = (grad_weight_dtype == CCE_DTYPE_F32) ? static_cast<void*>(static_cast<float*>(grad_weight) + v0 * d)
+                                                 : static_cast<void*>(static_cast<bf16_t*>(grad_weight) + v0 * d);
+    e.ldo = d;
+    e.out_f32 = (grad_weight_dtype == CCE_DTYPE_F32);
+    e.mode = 0;
+  };
+  // WT[j][c] = W[v0 + c][j], zero for vb <= c < vb64
+  auto transpose_band = [&](long b) -> int {
+    long v0, vb, vb64;
+    band_cols(b, v0, vb, vb64);
+    hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)ceil_div(vb64, 64), (unsigned)ceil_div(d, 64)), dim3(256), 0,
+                       st, W + v0 * d, (long)d, (int)vb, (int)d, L.WT, (long)Vb, (int)vb64);
+    HIP_TRY(hipGetLastError());
+    return CCE_OK;
+  };
+  auto colsum_band = [&](long b, const bf16_t* G) -> int {
+    long v0, vb, vb64;
+    band_cols(b, v0, vb, vb64);
+    hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)ceil_div(vb, 64)), dim3(256), 0, st, G, (long)Vb, (int)N,
+                       (int)vb, grad_bias + v0);
+    HIP_TRY(hipGetLastError());
+    return CCE_OK;
+  };
+
+  if (banded(d)) {
+    // launch b: dW(b), dH(b) from G[b & 1] and the recompute of band b+1 into
+    // G[(b+1) & 1]; band 0's recompute runs alone first.
+    const long dmain = (d % 256 == 0 || d % 256 > 128) ? d : d - d % 256;
+    {
+      long v0, vb, vb64;
+      band_cols(0, v0, vb, vb64);
+      GemmShape g1 = {};
+      GradParams e1 = {};
+      int nb1 = 0;
+      grad_shape(H, W, bias, L, L.G[0], N, d, Vb, v0, vb, kFastBN, g1, e1, nb1);
+      rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiGradBias, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false)
+                : launch_gemm<kFastBN, kWarp8, true, true, EpiGrad, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false);
+      if (rc) return rc;
+    }
+    for (long b = 0; b < nbands; ++b) {
+      const bf16_t* G = L.G[b & 1];
+      BandLaunch p = {};
+      if (need_dw) {
+        dw_shape(b, G, p.dw, p.e_dw);
+        p.nb_dw = (int)(ceil_div(p.dw.M, kBM) * ceil_div(p.dw.N, kSlowBN));
+      }
+      if (need_dh) {
+        rc = transpose_band(b);
+        if (rc) return rc;
+        if (dmain > 0) {
+          dh_shape(b, G, 0, dmain, p.dh, p.e_dh);
+          p.nb_dh = gm * (int)ceil_div(dmain, kFastBN);
+        }
+        if (dmain < d) {
+          dh_shape(b, G, dmain, d - dmain, p.dh2, p.e_dh2);
+          p.nb_dh2 = gm * (int)ceil_div(d - dmain, kSlowBN);
+        }
+      }
+      if (b + 1 < nbands) {
+        long v0, vb, vb64;
+        band_cols(b + 1, v0, vb, vb64);
+        grad_shape(H, W, bias, L, L.G[(b + 1) & 1], N, d, Vb, v0, vb, kFastBN, p.gr, p.e_gr, p.nb_gr);
+      }
+      rc = launch_band(p, bias != nullptr, st);
+      if (rc) return rc;
+      if (need_db) {
+        rc = colsum_band(b, G);
+        if (rc) return rc;
+      }
+    }
+    return CCE_OK;
+  }
+
+  // d not a multiple of 64: one G buffer; per band the recompute (register-
+  // staged pipeline), then dH and dW
   for (long b = 0; b < nbands; ++b) {
-    const long v0 = b * Vb;
-    const long vb = (V - v0 < Vb) ? (V - v0) : Vb;
-    const long vb64 = (long)align_up((size_t)vb, 64);
-
-    // G = dLoss/dS for columns [v0, v0 + vb)
-    GemmShape g1;
-    g1.A = H; g1.lda = d; g1.B = W + v0 * d; g1.ldb = d;
-    g1.M = (int)N; g1.N = (int)vb; g1.K = (int)d;
-    GradParams e1;
-    e1.bias = bias; e1.rowp = L.rowp; e1.rowlab = L.rowlab; e1.G = L.G; e1.ldg = Vb; e1.v0 = (int)v0;
-    const int gbn = fast_k(d) ? kFastBN : kSlowBN;
-    e1.tiles_n = (int)ceil_div(vb, gbn);
-    e1.splits = (int)std::min<long>(e1.tiles_n, std::max<long>(1, ceil_div(CCE_GRAD_WGS, gm)));
-    const int nb1 = gm * e1.splits;
-    if (fast_k(d))
-      rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiGradBias, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD)
-                : launch_gemm<kFastBN, kWarp8, true, true, EpiGrad, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD);
-    else
-      rc = bias ? launch_gemm<kSlowBN, kWarp8, true, true, EpiGradBias, 3>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD)
-                : launch_gemm<kSlowBN, kWarp8, true, true, EpiGrad, 3>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD);
+    long v0, vb, vb64;
+    band_cols(b, v0, vb, vb64);
+    GemmShape g1 = {};
+    GradParams e1 = {};
+    int nb1 = 0;
+    grad_shape(H, W, bias, L, L.G[0], N, d, Vb, v0, vb, kSlowBN, g1, e1, nb1);
+    rc = bias ? launch_gemm<kSlowBN, kWarp8, true, true, EpiGradBias, 3>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false)
+              : launch_gemm<kSlowBN, kWarp8, true, true, EpiGrad, 3>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false);
     if (rc) return rc;
-
     GemmShape g2 = {}, g3 = {};
     AccParams e2 = {}, e3 = {};
     if (need_dh) {
-      // WT[j][c] = W[v0 + c][j], zero for vb <= c < vb64
-      hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)ceil_div(vb64, 64), (unsigned)ceil_div(d, 64)), dim3(256),
-                         0, st, W + v0 * d, (long)d, (int)vb, (int)d, L.WT, (long)Vb, (int)vb64);
-      HIP_TRY(hipGetLastError());
-      g2.A = L.G; g2.lda = Vb; g2.B = L.WT; g2.ldb = Vb;
-      g2.M = (int)N; g2.N = (int)d; g2.K = (int)vb64;
-      e2.acc32 = L.dHacc; e2.ldacc = d; e2.out = grad_hidden; e2.ldo = d;
-      e2.out_f32 = (grad_hidden_dtype == CCE_DTYPE_F32);
-      e2.mode = (nbands == 1) ? 0 : (b == 0 ? 1 : (b == nbands - 1 ? 3 : 2));
+      rc = transpose_band(b);
+      if (rc) return rc;
+      dh_shape(b, L.G[0], 0, d, g2, e2);
     }
-    if (need_dw) {
-      g3.A = L.G; g3.lda = Vb;  // MN-major: element (v, n) at G[n*Vb + v]
-      g3.B = L.HT; g3.ldb = N8;
-      g3.M = (int)vb; g3.N = (int)d; g3.K = (int)N;
-      e3.acc32 = nullptr; e3.ldacc = 0;
-      e3.out = (grad_weight_dtype == CCE_DTYPE_F32)
-                   ? static_cast<void*>(static_cast<float*>(grad_weight) + v0 * d)
-                   : static_cast<void*>(static_cast<bf16_t*>(grad_weight) + v0 * d);
-      e3.ldo = d;
-      e3.out_f32 = (grad_weight_dtype == CCE_DTYPE_F32);
-      e3.mode = 0;
-    }
+    if (need_dw) dw_shape(b, L.G[0], g3, e3);
     if (need_dh && need_dw)
       rc = launch_dual_acc(g3, e3, g2, e2, st);
     else if (need_dh)
@@ -1543,9 +1711,8 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       rc = launch_acc<kSlowBN, false, 5>(g3, e3, st, CCE_KERNEL_BWD_DW);
     if (rc) return rc;
     if (need_db) {
-      hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)ceil_div(vb, 64)), dim3(256), 0, st, L.G, (long)Vb, (int)N,
-                         (int)vb, grad_bias + v0);
-      HIP_TRY(hipGetLastError());
+      rc = colsum_band(b, L.G[0]);
+      if (rc) return rc;
     }
   }
   return CCE_OK;
@@ -1558,35 +1725,40 @@ int cce_kernel_timing_enable(int enable) {
   return CCE_OK;
 }
 
-int cce_kernel_timing_read(int kind, double* total_ms, int64_t* launches) {
+int cce_kernel_timing_read(int kind, double* total_ms, int64_t* launches, double* credited_flops,
+                           double* executed_flops) {
   g_err[0] = 0;
   if (kind < 0 || kind >= CCE_KERNEL_KINDS) return fail(CCE_ERR_INVALID_ARG, "kernel kind %d out of range", kind);
   if (!total_ms || !launches) return fail(CCE_ERR_INVALID_ARG, "total_ms and launches must not be null");
-  std::vector<std::pair<hipEvent_t, hipEvent_t>> recs;
+  std::vector<TimedLaunch> recs;
   {
     std::lock_guard<std::mutex> lk(g_timing.mu);
     recs.swap(g_timing.pending[kind]);
   }
-  double sum = 0.0;
+  double sum = 0.0, cr = 0.0, ex = 0.0;
   int rc = CCE_OK;
   for (auto& r : recs) {
     float ms = 0.f;
     if (rc == CCE_OK) {
-      hipError_t e = hipEventSynchronize(r.second);
-      if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.first, r.second);
+      hipError_t e = hipEventSynchronize(r.ev1);
+      if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.ev0, r.ev1);
       if (e != hipSuccess) rc = fail(CCE_ERR_HIP, "kernel timing: %s", hipGetErrorString(e));
     }
     sum += ms;
+    cr += r.credited;
+    ex += r.executed;
   }
   {
     std::lock_guard<std::mutex> lk(g_timing.mu);
     for (auto& r : recs) {
-      g_timing.pool.push_back(r.first);
-      g_timing.pool.push_back(r.second);
+      g_timing.pool.push_back(r.ev0);
+      g_timing.pool.push_back(r.ev1);
     }
   }
   *total_ms = sum;
   *launches = (int64_t)recs.size();
+  if (credited_flops) *credited_flops = cr;
+  if (executed_flops) *executed_flops = ex;
   return rc;
 }
 

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define CCE_ABI_VERSION 1
+#define CCE_ABI_VERSION 2
 
 #define CCE_OK 0
 #define CCE_ERR_INVALID_ARG 1
@@ -110,17 +110,24 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
  * Per-kernel timing for measurement tools (no counterpart in the reference).
  * While enabled, every GEMM launch of cce_forward / cce_backward is bracketed
  * by HIP events recorded on its stream.  cce_kernel_timing_read() waits for
- * the recorded events, returns the summed milliseconds and launch count of
- * one kernel kind and clears that kind's record.  Kinds:
+ * the recorded events and returns, for one kernel kind, the summed
+ * milliseconds, the launch count and the MFMA FLOPs of those launches —
+ * credited (the algorithmic work: forward logits, dHidden, dWeight; the
+ * backward's logits recompute is executed but not credited) and executed —
+ * then clears that kind's record.  credited_flops / executed_flops may be
+ * NULL.  Kinds:
  */
-#define CCE_KERNEL_FWD_LSE 0   /* forward GEMM + online logsumexp        */
-#define CCE_KERNEL_BWD_GRAD 1  /* backward recompute GEMM -> dLoss/dS     */
-#define CCE_KERNEL_BWD_DH 2    /* dHidden GEMM (per vocabulary band)      */
-#define CCE_KERNEL_BWD_DW 3    /* dWeight GEMM (per vocabulary band)      */
-#define CCE_KERNEL_BWD_DHDW 4  /* dHidden + dWeight GEMMs in one launch   */
-#define CCE_KERNEL_KINDS 5
+#define CCE_KERNEL_FWD_LSE 0   /* forward GEMM + online logsumexp                 */
+#define CCE_KERNEL_BWD_GRAD 1  /* backward recompute GEMM -> dLoss/dS             */
+#define CCE_KERNEL_BWD_DH 2    /* dHidden GEMM (per vocabulary band)               */
+#define CCE_KERNEL_BWD_DW 3    /* dWeight GEMM (per vocabulary band)               */
+#define CCE_KERNEL_BWD_DHDW 4  /* dHidden + dWeight GEMMs in one launch            */
+#define CCE_KERNEL_BWD_BAND 5  /* dHidden + dWeight of band b with the recompute
+                                  of band b+1 in one launch                        */
+#define CCE_KERNEL_KINDS 6
 int cce_kernel_timing_enable(int enable);
-int cce_kernel_timing_read(int kind, double* total_ms, int64_t* launches);
+int cce_kernel_timing_read(int kind, double* total_ms, int64_t* launches, double* credited_flops,
+                           double* executed_flops);
 
 #ifdef __cplusplus
 }

@@ -66,8 +66,23 @@ def test_no_undeclared_exports():
 def test_constants_match_header():
     for name in ("CCE_ABI_VERSION", "CCE_OK", "CCE_ERR_INVALID_ARG", "CCE_ERR_WORKSPACE", "CCE_ERR_HIP",
                  "CCE_REDUCTION_NONE", "CCE_REDUCTION_MEAN", "CCE_REDUCTION_SUM", "CCE_DTYPE_BF16",
-                 "CCE_DTYPE_F32"):
+                 "CCE_DTYPE_F32", "CCE_KERNEL_FWD_LSE", "CCE_KERNEL_BWD_GRAD", "CCE_KERNEL_BWD_DH",
+                 "CCE_KERNEL_BWD_DW", "CCE_KERNEL_BWD_DHDW", "CCE_KERNEL_BWD_BAND", "CCE_KERNEL_KINDS"):
         assert getattr(_lib, name) == header_define(name), name
+    assert sorted(_lib.KERNEL_KIND_NAMES) == list(range(_lib.CCE_KERNEL_KINDS))
+
+
+def test_kernel_timing_hook_without_launches(lib):
+    # nothing recorded: zero time, launches and FLOPs, no device call
+    for k in range(_lib.CCE_KERNEL_KINDS):
+        assert _lib.kernel_timing_read(k) == (0.0, 0, 0.0, 0.0)
+    with pytest.raises(_lib.CCEError, match="out of range"):
+        _lib.kernel_timing_read(_lib.CCE_KERNEL_KINDS)
+    import ctypes
+    ms, n = ctypes.c_double(), ctypes.c_int64()
+    # the FLOP outputs are optional
+    assert lib.cce_kernel_timing_read(0, ctypes.byref(ms), ctypes.byref(n), None, None) == _lib.CCE_OK
+    assert lib.cce_kernel_timing_read(0, None, ctypes.byref(n), None, None) == _lib.CCE_ERR_INVALID_ARG
 
 
 def test_abi_version(lib):

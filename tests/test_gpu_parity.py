@@ -83,6 +83,8 @@ def _rand_case(N, d, V, seed=0, ignore_frac=0.1, bias=False, wscale=0.05):
     (257, 136, 1000, 512),     # d not a multiple of 64, ragged bands
     (600, 128, 5000, 1024),
     (513, 264, 3001, 8192),
+    (300, 192, 2100, 512),     # d % 256 > 128: one padded 256-wide dH column tile
+    (333, 320, 1500, 768),     # d = 256 + 64: 256-wide dH tile plus a 128-wide tail tile
 ])
 def test_ragged_shapes(gpu, N, d, V, chunk):
     print(f"case N={N} d={d} V={V} chunk={chunk}", flush=True)
@@ -143,6 +145,23 @@ def test_frozen_weight_and_int32_labels_and_3d(gpu):
     assert got["dw"] is None
     assert_loss_close(got["loss"], ref["loss"])
     assert_grad_close(got["dh"].reshape(ref["dh"].shape), ref["dh"], "dh (frozen W)")
+
+
+@pytest.mark.parametrize("need_dh,need_dw,need_db", [(True, False, False), (False, True, False),
+                                                    (False, False, True), (False, True, True)])
+def test_gradient_subsets_banded(gpu, need_dh, need_dw, need_db):
+    """Every subset of requested gradients through the banded backward (d % 64 == 0, several
+    bands, so the per-band launch alternates its two G buffers)."""
+    print(f"case dh={need_dh} dw={need_dw} db={need_db}", flush=True)
+    h, w, lab, b = _rand_case(450, 384, 2600, seed=31, bias=True)
+    got = run_hip(gpu, h, w, lab, b, chunk=512, need_dh=need_dh, need_dw=need_dw, need_db=need_db)
+    ref = run_oracle(h, w, lab, b, chunk=512)
+    assert_loss_close(got["loss"], ref["loss"])
+    for k, need in (("dh", need_dh), ("dw", need_dw), ("db", need_db)):
+        if need:
+            assert_grad_close(got[k], ref[k], f"{k} (subset)")
+        else:
+            assert got[k] is None
 
 
 def test_fp32_and_fp16_inputs_return_input_dtypes(gpu):
