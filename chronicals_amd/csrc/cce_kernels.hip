@@ -932,21 +932,24 @@ __global__ __launch_bounds__(W * 64) void dual_acc_kernel(GemmShape g_dw, AccPar
 
 // One launch per vocabulary band b of the backward (d a multiple of 64): the
 // dW and dH GEMMs of band b and the logits recompute of band b+1, which
-// writes the other G buffer.  Workgroups are numbered longest first — dW
-// (K = N), dH (K = band width; d in 256-wide column tiles plus one 128-wide
-// tail tile when d % 256 <= 128, so no MFMA work is spent on padding), then
-// the short recompute tiles — so the recompute fills the CUs the long tiles
-// leave idle at the end of the band.
+// writes the other G buffer.  Both gradient GEMMs tile d in 256-wide column
+// tiles plus one 128-wide tail tile when d % 256 <= 128 (no MFMA work spent
+// on padding, and the wide tiles do the most work per CU-second).
+// Workgroups are numbered longest first — dW (K = N), dH (K = band width),
+// then the short recompute tiles, which fill the CUs the long tiles leave
+// idle at the end of the band.
 struct BandLaunch {
   GemmShape dw;
   AccParams e_dw;
+  GemmShape dw2;
+  AccParams e_dw2;
   GemmShape dh;
   AccParams e_dh;
   GemmShape dh2;
   AccParams e_dh2;
   GemmShape gr;
   GradParams e_gr;
-  int nb_dw, nb_dh, nb_dh2, nb_gr;
+  int nb_dw, nb_dw2, nb_dh, nb_dh2, nb_gr;
 };
 
 template <bool HB>
@@ -954,10 +957,15 @@ __global__ __launch_bounds__(kWarp8 * 64) void band_kernel(BandLaunch p) {
   __shared__ __attribute__((aligned(16))) bf16_t smem[2 * (kBM + kFastBN) * 64];
   int b = blockIdx.x;
   if (b < p.nb_dw) {
-    gemm_body<kSlowBN, kWarp8, false, true, EpiAcc, 5>(p.dw, p.e_dw, b, p.nb_dw, smem);
+    gemm_body<kFastBN, kWarp8, false, true, EpiAcc, 5>(p.dw, p.e_dw, b, p.nb_dw, smem);
     return;
   }
   b -= p.nb_dw;
+  if (b < p.nb_dw2) {
+    gemm_body<kSlowBN, kWarp8, false, true, EpiAcc, 5>(p.dw2, p.e_dw2, b, p.nb_dw2, smem);
+    return;
+  }
+  b -= p.nb_dw2;
   if (b < p.nb_dh) {
     gemm_body<kFastBN, kWarp8, true, true, EpiAcc, 4>(p.dh, p.e_dh, b, p.nb_dh, smem);
     return;
@@ -1412,7 +1420,7 @@ void grad_shape(const bf16_t* H, const bf16_t* W, const float* bias, const BwdLa
 }
 
 int launch_band(const BandLaunch& p, bool has_bias, hipStream_t st) {
-  const int nb = p.nb_dw + p.nb_dh + p.nb_dh2 + p.nb_gr;
+  const int nb = p.nb_dw + p.nb_dw2 + p.nb_dh + p.nb_dh2 + p.nb_gr;
   if (nb <= 0) return CCE_OK;
   hipEvent_t t0 = nullptr, t1 = nullptr;
   const bool timed = timing_begin(st, &t0, &t1);
@@ -1424,6 +1432,7 @@ int launch_band(const BandLaunch& p, bool has_bias, hipStream_t st) {
   if (timed) {
     double cr = 0.0;
     if (p.nb_dw) cr += gemm_flops(p.dw.M, p.dw.N, p.dw.K);
+    if (p.nb_dw2) cr += gemm_flops(p.dw2.M, p.dw2.N, p.dw2.K);
     if (p.nb_dh) cr += gemm_flops(p.dh.M, p.dh.N, p.dh.K);
     if (p.nb_dh2) cr += gemm_flops(p.dh2.M, p.dh2.N, p.dh2.K);
     const double ex = cr + (p.nb_gr ? gemm_flops(p.gr.M, p.gr.N, p.gr.K) : 0.0);
@@ -1602,16 +1611,18 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     e.out_f32 = (grad_hidden_dtype == CCE_DTYPE_F32);
     e.mode = (nbands == 1) ? 0 : (b == 0 ? 1 : (b == nbands - 1 ? 3 : 2));
   };
-  // dW of one band: rows [v0, v0 + vb) of grad_weight = G^T . H
-  auto dw_shape = [&](long b, const bf16_t* G, GemmShape& g, AccParams& e) {
+  // dW of one band: rows [v0, v0 + vb), hidden columns [c0, c0 + nc) of
+  // grad_weight = G^T . H
+  auto dw_shape = [&](long b, const bf16_t* G, long c0, long nc, GemmShape& g, AccParams& e) {
     long v0, vb, vb64;
     band_cols(b, v0, vb, vb64);
     g.A = G; g.lda = Vb;  // MN-major: element (v, n) at G[n*Vb + v]
-    g.B = L.HT; g.ldb = N8;
-    g.M = (int)vb; g.N = (int)d; g.K = (int)N;
+    g.B = L.HT + c0 * N8; g.ldb = N8;
+    g.M = (int)vb; g.N = (int)nc; g.K = (int)N;
     e.acc32 = nullptr; e.ldacc = 0;
-    e.out = (grad_weight_dtype == CCE_DTYPE_F32) ? static_cast<void*>(static_cast<float*>(grad_weight) + v0 * d)
-                                                 : static_cast<void*>(static_cast<bf16_t*>(grad_weight) + v0 * d);
+    const long o = v0 * d + c0;
+    e.out = (grad_weight_dtype == CCE_DTYPE_F32) ? static_cast<void*>(static_cast<float*>(grad_weight) + o)
+                                                 : static_cast<void*>(static_cast<bf16_t*>(grad_weight) + o);
     e.ldo = d;
     e.out_f32 = (grad_weight_dtype == CCE_DTYPE_F32);
     e.mode = 0;
@@ -1653,8 +1664,14 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       const bf16_t* G = L.G[b & 1];
       BandLaunch p = {};
       if (need_dw) {
-        dw_shape(b, G, p.dw, p.e_dw);
-        p.nb_dw = (int)(ceil_div(p.dw.M, kBM) * ceil_div(p.dw.N, kSlowBN));
+        if (dmain > 0) {
+          dw_shape(b, G, 0, dmain, p.dw, p.e_dw);
+          p.nb_dw = (int)(ceil_div(p.dw.M, kBM) * ceil_div(dmain, kFastBN));
+        }
+        if (dmain < d) {
+          dw_shape(b, G, dmain, d - dmain, p.dw2, p.e_dw2);
+          p.nb_dw2 = (int)(ceil_div(p.dw2.M, kBM) * ceil_div(d - dmain, kSlowBN));
+        }
       }
       if (need_dh) {
         rc = transpose_band(b);
@@ -1702,7 +1719,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       if (rc) return rc;
       dh_shape(b, L.G[0], 0, d, g2, e2);
     }
-    if (need_dw) dw_shape(b, L.G[0], g3, e3);
+    if (need_dw) dw_shape(b, L.G[0], 0, d, g3, e3);
     if (need_dh && need_dw)
       rc = launch_dual_acc(g3, e3, g2, e2, st);
     else if (need_dh)
