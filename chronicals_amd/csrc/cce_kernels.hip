@@ -266,6 +266,10 @@ __device__ inline void pin_epilogue(int& l, int& tm, int& tn) {
 // ---------------------------------------------------------------------------
 __device__ inline int swz(int r) { return (r ^ (r >> 3)) & 7; }
 
+// s_waitcnt immediate for vmcnt(n) alone (expcnt and lgkmcnt at their no-wait
+// maxima): vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8].
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
 __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, long bytes) {
   const long cap = 0x7ffffff0L;
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)(bytes < cap ? bytes : cap),
@@ -426,15 +430,17 @@ struct EpiLseT {
     t0 = (int)(((long)p.tiles_n * s) / p.splits);
     t1 = (int)(((long)p.tiles_n * (s + 1)) / p.splits);
   }
-  static __device__ inline void init(State& st) {
+  static constexpr int kStores = 0;  // global stores a tile epilogue issues per wave
+  static __device__ inline void init(const Params&, State& st, const GemmShape&, int, int, int) {
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       st.m[i] = kNegBig;
       st.s[i] = 0.f;
     }
   }
+  static constexpr int kScratch = 0;  // LDS elements the epilogue stages through
   static __device__ inline void tile(const Params& p, State& st, WaveAcc<BN, W>& acc, const GemmShape& g, int tm,
-                                     int tn, int wm, int wn, int l) {
+                                     int tn, int wm, int wn, int l, bf16_t*) {
     constexpr int FN = BN / 64;
     pin_epilogue(l, tm, tn);
     const int c0 = tn * BN;
@@ -542,6 +548,13 @@ struct GradParams {
 
 // Backward recompute: G[n][c] = dLoss/dS for one vocabulary band, stored bf16.
 // rowp[n] = {lse*log2e, cP, cT, cU}: g = cP*2^(x*log2e - lse2) - cU - cT*[c == label].
+//
+// Stores go through LDS: in the MFMA layout a lane holds one row, so a direct
+// store instruction would touch 32 rows with 16 bytes each.  Each wave writes
+// a 32 x 64 block into its own 4 KB of LDS (8-byte pieces, XOR-swizzled by
+// row so the 16 lanes of a write phase hit distinct banks), reads it back
+// row-major and stores whole 128-byte row segments, 8 rows per instruction.
+// A wave's LDS operations execute in order, so no barrier is needed.
 template <int BN, int W, bool HB>
 struct EpiGradT {
   typedef GradParams Params;
@@ -549,7 +562,20 @@ struct EpiGradT {
   // tile's loads are in flight while this tile's epilogue runs.
   static constexpr bool kMultiTile = true;
   static constexpr int FM = WaveCfg<W>::kFM;
-  struct State {};
+  static constexpr int kScratch = W * 2048;  // 32 x 64 bf16 per wave
+  // Without bias the tile epilogue issues exactly kStores buffer stores per
+  // wave and no other vector memory operation (rows past M fall outside the
+  // store descriptor and are dropped, so no wave branches around a store);
+  // the per-row parameters are loaded once per workgroup (its row tile is
+  // fixed), since a load issued after a tile's stores would wait for all of
+  // them.  With bias the epilogue loads bias values, and its stores are
+  // waited for in full at the next barrier (kStores = 0).
+  static constexpr int kStores = HB ? 0 : FM * (BN / 128) * 4;
+  static constexpr int kRows = HB ? 1 : FM;
+  struct State {
+    float4 rp[kRows];
+    int lab[kRows];
+  };
   static __device__ inline void assign(const GemmShape& g, const Params& p, int bid, int nb, int& tm, int& t0,
                                        int& t1, int& split) {
     const int gm = (g.M + kBM - 1) / kBM;
@@ -559,38 +585,77 @@ struct EpiGradT {
     t0 = (int)(((long)p.tiles_n * s) / p.splits);
     t1 = (int)(((long)p.tiles_n * (s + 1)) / p.splits);
   }
-  static __device__ inline void init(State&) {}
-  static __device__ inline void tile(const Params& p, State&, WaveAcc<BN, W>& acc, const GemmShape& g, int tm,
-                                     int tn, int wm, int wn, int l) {
+  static __device__ inline void row_params(const Params& p, const GemmShape& g, int m, float4& rp, int& lab) {
+    const int mc = m < g.M ? m : 0;
+    rp = p.rowp[mc];
+    lab = p.rowlab[mc] - p.v0;
+  }
+  static __device__ inline void init(const Params& p, State& st, const GemmShape& g, int tm, int wm, int l) {
+    if constexpr (!HB) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) row_params(p, g, tm * kBM + acc_row<W>(wm, i, l), st.rp[i], st.lab[i]);
+    }
+  }
+  static __device__ inline void tile(const Params& p, State& st, WaveAcc<BN, W>& acc, const GemmShape& g, int tm,
+                                     int tn, int wm, int wn, int l, bf16_t* scratch) {
     constexpr int FN = BN / 64;
+    static_assert(FN % 2 == 0, "64-column staging blocks");
     pin_epilogue(l, tm, tn);
+    bf16_t* const ws = scratch + (wm * 2 + wn) * 2048;
+    const int r = l & 31;
+    // this row tile of G: rows past M are out of the descriptor's range
+    const int rows = min(g.M - tm * kBM, kBM);
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(p.G + (long)tm * kBM * p.ldg, (long)rows * p.ldg * 2);
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int m = tm * kBM + acc_row<W>(wm, i, l);
-      if (m >= g.M) continue;
-      const float4 rp = p.rowp[m];
-      const int lab = p.rowlab[m] - p.v0;
+      const bool mok = m < g.M;
+      float4 rp;
+      int lab;
+      if constexpr (HB) {
+        row_params(p, g, m, rp, lab);
+      } else {
+        rp = st.rp[i];
+        lab = st.lab[i];
+      }
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
+      for (int jp = 0; jp < FN / 2; ++jp) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int cb = tn * BN + acc_col<BN>(wn, j, q, l);
-          float gv[4];
+        for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int col = cb + e;
-            float gg = 0.f;
-            if (col < g.N) {
-              const float b = HB ? p.bias[p.v0 + col] : 0.f;
-              const float x = (acc.v[i][j][4 * q + e] + b) * kLog2e - rp.x;
-              gg = rp.y * fast_exp2(x) - rp.w;
-              if (col == lab) gg -= rp.z;
+          for (int q = 0; q < 4; ++q) {
+            const int cb = tn * BN + acc_col<BN>(wn, 2 * jp + jj, q, l);
+            float gv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int col = cb + e;
+              float gg = 0.f;
+              if (mok && col < g.N) {
+                const float b = HB ? p.bias[p.v0 + col] : 0.f;
+                const float x = (acc.v[i][2 * jp + jj][4 * q + e] + b) * kLog2e - rp.x;
+                gg = rp.y * fast_exp2(x) - rp.w;
+                if (col == lab) gg -= rp.z;
+              }
+              gv[e] = gg;
             }
-            gv[e] = gg;
+            // 8-byte piece hc (of 16 per 128-byte row) lives at hc ^ (row & 15)
+            const int hc = (jj * 8 + 2 * q + (l >> 5)) ^ (r & 15);
+            *reinterpret_cast<u32x2*>(ws + r * 64 + hc * 4) =
+                u32x2{pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3])};
           }
-          const u32x2 pk = {pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3])};
-          *reinterpret_cast<u32x2*>(p.G + (long)m * p.ldg + cb) = pk;
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int rr = t * 8 + (l >> 3), c = l & 7;
+          // 16-byte chunk c = pieces 2c, 2c+1, stored at slot c ^ ((rr & 14) >> 1), halves swapped for odd rows
+          u32x4 v = *reinterpret_cast<const u32x4*>(ws + rr * 64 + ((c ^ ((rr & 14) >> 1)) << 3));
+          if (rr & 1) v = u32x4{v[2], v[3], v[0], v[1]};
+          const int trow = wm * WaveCfg<W>::kWaveRows + i * 32 + rr;
+          const int gcol = tn * BN + wn * (BN / 2) + jp * 64 + c * 8;
+          __builtin_amdgcn_raw_buffer_store_b128(v, gr, (int)(((long)trow * p.ldg + gcol) * 2), 0, 0);
         }
+        asm volatile("" ::: "memory");
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -620,6 +685,7 @@ struct EpiAcc {
   typedef AccParams Params;
   static constexpr bool kMultiTile = false;
   static constexpr int FM = WaveCfg<W>::kFM;
+  static constexpr int kScratch = 0;
   struct State {};
   static __device__ inline void assign(const GemmShape& g, const Params&, int bid, int nb, int& tm, int& t0,
                                        int& t1, int& split) {
@@ -630,9 +696,10 @@ struct EpiAcc {
     t1 = tn + 1;
     split = 0;
   }
-  static __device__ inline void init(State&) {}
+  static constexpr int kStores = 0;  // single-tile workgroups: nothing follows the epilogue
+  static __device__ inline void init(const Params&, State&, const GemmShape&, int, int, int) {}
   static __device__ inline void tile(const Params& p, State&, WaveAcc<BN, W>& acc, const GemmShape& g, int tm,
-                                     int tn, int wm, int wn, int l) {
+                                     int tn, int wm, int wn, int l, bf16_t*) {
     constexpr int FN = BN / 64;
     pin_epilogue(l, tm, tn);
 #pragma unroll
@@ -681,11 +748,20 @@ struct EpiAcc {
 // on across tile boundaries.  Single-tile epilogues peel the last slab pair so
 // no prefetch registers are live while they run.
 // ---------------------------------------------------------------------------
+// LDS elements of the pipeline stages: unpadded for the direct-to-LDS
+// pipelines, kPitch-padded rows for the register-staged ones.
+template <int BN>
+constexpr int gemm_lds_elems(int pipe) {
+  return 2 * (kBM + BN) * (pipe >= 4 ? 64 : kPitch);
+}
+
 template <int BN, int W, bool AK, bool BKM, template <int, int> class EpiT, int PIPE>
 __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename EpiT<BN, W>::Params& ep, int bid,
                                           int nb, bf16_t* smem) {
   typedef EpiT<BN, W> Epi;
   constexpr int kStage = (kBM + BN) * kPitch;
+  // epilogue staging area, past the pipeline's LDS stages
+  bf16_t* const scratch = smem + gemm_lds_elems<BN>(PIPE);
 
   const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
   const int wm = w >> 1, wn = w & 1;
@@ -695,7 +771,7 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
   if (t0 >= t1) return;  // uniform for the whole workgroup
 
   typename Epi::State st;
-  Epi::init(st);
+  Epi::init(ep, st, g, tm, wm, l);
   WaveAcc<BN, W> acc;
 
   const int KT = (g.K + kBK - 1) / kBK;
@@ -745,9 +821,16 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
     // reliably wait for them, so each barrier that publishes a slab is
     // preceded by an explicit vmcnt(0).  sched_barrier fences keep the MFMAs
     // on their side of it.
-    auto publish = [&]() {
+    // At the first barrier of a tile the previous tile's epilogue stores
+    // (issued after this slab's DMA; vector memory operations retire in
+    // issue order) may stay in flight: they drain behind the MFMAs instead of
+    // stalling the workgroup.
+    auto publish = [&](bool after_epilogue) {
       __builtin_amdgcn_sched_barrier(0);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (Epi::kStores > 0 && after_epilogue)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(Epi::kStores));
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       __builtin_amdgcn_sched_barrier(0);
     };
@@ -761,7 +844,7 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
     const int total = (t1 - t0) * KT;
     issue(T0);
     if (total > 1) issue(T1);
-    publish();
+    publish(false);
     Frags<BN, W> fa, fb;
     frags(T0, 0, fa);
     int s = 0;
@@ -779,14 +862,14 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
         frags(Sc, 3, fb);
         mfma_frags<BN, W>(fa, acc);
         order();
-        publish();         // B_s
+        publish(kt == 0 && tn != t0);  // B_s
         frags(Sn, 0, fa);  // past the last slab this reads stale data, unused
         mfma_frags<BN, W>(fb, acc);
         order();
         __builtin_amdgcn_sched_barrier(0);
         if (s + 2 < total) issue(Sc);
       }
-      Epi::tile(ep, st, acc, g, tm, tn, wm, wn, l);
+      Epi::tile(ep, st, acc, g, tm, tn, wm, wn, l, scratch);
     }
     Epi::finish(ep, st, g, tm, split, smem, wm, wn, l);
     return;
@@ -829,7 +912,7 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
         }
         __syncthreads();
       }
-      Epi::tile(ep, st, acc, g, tm, tn, wm, wn, l);
+      Epi::tile(ep, st, acc, g, tm, tn, wm, wn, l, scratch);
     }
     Epi::finish(ep, st, g, tm, split, smem, wm, wn, l);
     return;
@@ -904,14 +987,14 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
       slab(I0{}, F{}, T{}, T{}, 0, 0);
       slab(I1{}, F{}, F{}, F{}, 0, 0);
     }
-    Epi::tile(ep, st, acc, g, tm, tn, wm, wn, l);
+    Epi::tile(ep, st, acc, g, tm, tn, wm, wn, l, scratch);
   }
   Epi::finish(ep, st, g, tm, split, smem, wm, wn, l);
 }
 
 template <int BN, int W, bool AK, bool BKM, template <int, int> class EpiT, int PIPE>
 __global__ __launch_bounds__(W * 64) void gemm_kernel(GemmShape g, typename EpiT<BN, W>::Params ep) {
-  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * (kBM + BN) * kPitch];
+  __shared__ __attribute__((aligned(16))) bf16_t smem[gemm_lds_elems<BN>(PIPE) + EpiT<BN, W>::kScratch];
   gemm_body<BN, W, AK, BKM, EpiT, PIPE>(g, ep, blockIdx.x, gridDim.x, smem);
 }
 
@@ -954,7 +1037,7 @@ struct BandLaunch {
 
 template <bool HB>
 __global__ __launch_bounds__(kWarp8 * 64) void band_kernel(BandLaunch p) {
-  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * (kBM + kFastBN) * 64];
+  __shared__ __attribute__((aligned(16))) bf16_t smem[gemm_lds_elems<kFastBN>(4) + EpiGrad<kFastBN, kWarp8>::kScratch];
   int b = blockIdx.x;
   if (b < p.nb_dw) {
     gemm_body<kFastBN, kWarp8, false, true, EpiAcc, 5>(p.dw, p.e_dw, b, p.nb_dw, smem);
