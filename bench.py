@@ -130,17 +130,22 @@ def main() -> int:
         _lib.kernel_timing_read(k)  # drop anything recorded so far
     base_mem = torch.cuda.memory_allocated()
     torch.cuda.reset_peak_memory_stats()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    # one event between consecutive steps: the mean over the K steps is the
+    # headline, the per-step spread is reported beside it
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     _lib.kernel_timing_enable(True)
     torch.cuda.synchronize()
-    start.record()
-    for _ in range(args.steps):
+    evs[0].record()
+    for i in range(args.steps):
         loss = step()
-    end.record()
+        evs[i + 1].record()
     torch.cuda.synchronize()
     _lib.kernel_timing_enable(False)
-    ms = start.elapsed_time(end) / args.steps
+    ms = evs[0].elapsed_time(evs[-1]) / args.steps
+    step_ms = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps))
+
+    def pct(q):
+        return step_ms[min(len(step_ms) - 1, int(round(q * (len(step_ms) - 1))))]
     peak_extra = torch.cuda.max_memory_allocated() - base_mem
 
     # per-kernel breakdown with the library's own FLOP accounting per launch:
@@ -164,11 +169,13 @@ def main() -> int:
     kd = kernels[dom]
     achieved = kd["tflops_credited"]
     traffic = None
+    clock = None
     try:
         with open(TRAFFIC_FILE) as f:
             tr = json.load(f)
         if tr.get("config") == cfg.name and tr.get("kernel") == dom:
             traffic = tr.get("hbm_bytes_per_launch")
+            clock = tr.get("mfma_busy_and_clock", {}).get(dom, {}).get("clock_ghz")
     except (OSError, ValueError):
         pass
 
@@ -181,6 +188,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
+        "step_ms": {"median": pct(0.5), "p10": pct(0.1), "p90": pct(0.9)},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -193,6 +201,10 @@ def main() -> int:
         "step_tflops_algorithmic": step_tflops,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
+                     # the chip runs below its 2.4 GHz peak clock under this load (power-limited); the
+                     # clock the profile measured for this kernel, and the fraction of the peak at it
+                     "clock_ghz_profiled": clock,
+                     "frac_at_profiled_clock": (achieved / (PEAK_BF16_TFLOPS * clock / 2.4)) if clock else None,
                      "kernel": f"{dom}: credited (algorithmic) FLOPs per launch "
                                f"({kd['credited_gflop_per_launch']:.1f} GFLOP) over its HIP-event average launch "
                                f"time ({kd['avg_launch_us']:.1f} us, {kd['launches_per_step']:g} launches/step); "

@@ -88,14 +88,15 @@ __device__ inline float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bi
 // ---------------------------------------------------------------------------
 // Workgroup -> tile mapping.  The hardware deals consecutive workgroup ids to
 // the 8 XCDs round-robin; remap so that each XCD receives a contiguous range
-// of logical tiles, then walk logical tiles in groups of 4 row tiles so the
-// ~32 workgroups resident on one XCD share 4 row tiles of A and 8 column
-// tiles of B through that XCD's L2.
+// of logical tiles, then walk logical tiles in groups of G row tiles so the
+// ~32 workgroups resident on one XCD share G row tiles of A and 32/G column
+// tiles of B through that XCD's L2 (G = 4 by default; the forward, whose
+// K = d is short, measured best with G = 8).
 // ---------------------------------------------------------------------------
+template <int G = 4>
 __device__ inline void grouped_map(int bid, int nb, int gm, int gn, int& pm, int& pn) {
   const int per = nb >> 3;
   const int u = (bid < per * 8) ? ((bid & 7) * per + (bid >> 3)) : bid;
-  constexpr int G = 4;
   const int width = G * gn;
   const int grp = u / width;
   const int first = grp * G;
@@ -425,7 +426,7 @@ struct EpiLseT {
                                        int& t0, int& t1, int& split) {
     const int gm = (g.M + kBM - 1) / kBM;
     int s;
-    grouped_map(bid, nb, gm, p.splits, tm, s);
+    grouped_map<8>(bid, nb, gm, p.splits, tm, s);
     split = s;
     t0 = (int)(((long)p.tiles_n * s) / p.splits);
     t1 = (int)(((long)p.tiles_n * (s + 1)) / p.splits);

@@ -27,6 +27,7 @@ import torch
 import torch.nn as nn
 
 from .. import _lib
+from .. import ops as _ops  # noqa: F401  (registers chronicals_hip::cce_fwd / cce_bwd)
 
 # Constants of the reference module (cut_cross_entropy.py:45-56), kept for
 # import compatibility.  The chunk size is the vocabulary band width of the
@@ -66,19 +67,12 @@ def get_optimal_chunk_size(vocab_size: int, hidden_dim: int, available_vram_gb: 
     return max(256, 2 ** int(math.log2(optimal)))
 
 
-def _stream_handle(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
-
-
 def _as_bf16_rows(x: torch.Tensor) -> torch.Tensor:
-    """Contiguous, 16-byte aligned bf16 copy/view of a 2-D tensor."""
+    """Contiguous bf16 copy/view of a 2-D tensor (the op itself realigns a
+    storage offset that is not 16-byte aligned)."""
     if x.dtype != torch.bfloat16:
         x = x.to(torch.bfloat16)
-    if not x.is_contiguous() or x.data_ptr() % 16 != 0:
-        x = x.contiguous()
-        if x.data_ptr() % 16 != 0:
-            x = x.clone()
-    return x
+    return x.contiguous()
 
 
 def _validate(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor, bias: Optional[torch.Tensor]):
@@ -119,30 +113,21 @@ def _reduction_code(reduction: str) -> int:
 
 
 def _forward_raw(hidden, weight, labels, bias, ignore_index, label_smoothing, z_loss_weight, red):
-    """One cce_forward call.  Returns (loss, lse, n_valid, h2, w2, lab, b32)."""
-    lib = _lib.load()
+    """Operand preparation + one chronicals_hip::cce_fwd call.
+
+    Returns (loss, lse, n_valid, h2, w2, lab, b32): the bf16 [N, d] / [V, d]
+    operands, flat labels and fp32 bias the backward reuses.
+    """
     _validate(hidden, weight, labels, bias)
-    device = hidden.device
     d = hidden.shape[-1]
-    V = weight.shape[0]
     h2 = _as_bf16_rows(hidden.detach().reshape(-1, d))
     w2 = _as_bf16_rows(weight.detach())
-    N = h2.shape[0]
     lab = labels.reshape(-1)
     if not lab.is_contiguous():
         lab = lab.contiguous()
     b32 = None if bias is None else bias.detach().to(torch.float32).contiguous()
-    with torch.cuda.device(device):
-        ws = torch.empty(_lib.forward_workspace_bytes(N, d, V, red), dtype=torch.uint8, device=device)
-        loss = torch.empty((N,) if red == _lib.CCE_REDUCTION_NONE else (1,), dtype=torch.float32, device=device)
-        lse = torch.empty((N,), dtype=torch.float32, device=device)
-        n_valid = torch.empty((1,), dtype=torch.int32, device=device)
-        _lib.check(lib.cce_forward(
-            h2.data_ptr(), w2.data_ptr(), lab.data_ptr(), int(lab.dtype == torch.int64),
-            b32.data_ptr() if b32 is not None else None,
-            N, d, V, int(ignore_index), float(label_smoothing), float(z_loss_weight), red,
-            loss.data_ptr(), lse.data_ptr(), n_valid.data_ptr(),
-            ws.data_ptr(), ws.numel(), _stream_handle(device)))
+    loss, lse, n_valid = torch.ops.chronicals_hip.cce_fwd(h2, w2, lab, b32, int(ignore_index), float(label_smoothing),
+                                                          float(z_loss_weight), int(red))
     return loss, lse, n_valid, h2, w2, lab, b32
 
 
@@ -169,7 +154,6 @@ class CutCrossEntropyFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output):
-        lib = _lib.load()
         h2, w2, lab, lse, n_valid, b32 = ctx.saved_tensors
         chunk_size, ignore_index, eps, zw, red = ctx.cfg
         hshape, hdtype, wdtype, bdtype = ctx.shapes
@@ -178,38 +162,13 @@ class CutCrossEntropyFunction(torch.autograd.Function):
         need_db = b32 is not None and ctx.needs_input_grad[3]
         if not (need_dh or need_dw or need_db):
             return (None,) * 9
-        device = h2.device
-        N, d = h2.shape
-        V = w2.shape[0]
-        g = grad_output.detach().to(torch.float32).reshape(-1).contiguous()
-        with torch.cuda.device(device):
-            dh = dw = db = None
-            if need_dh:
-                dh = torch.empty((N, d), dtype=torch.bfloat16 if hdtype == torch.bfloat16 else torch.float32,
-                                 device=device)
-            if need_dw:
-                dw = torch.empty((V, d), dtype=torch.bfloat16 if wdtype == torch.bfloat16 else torch.float32,
-                                 device=device)
-            if need_db:
-                db = torch.empty((V,), dtype=torch.float32, device=device)
-            ws = torch.empty(_lib.backward_workspace_bytes(N, d, V, chunk_size, need_dh, need_dw),
-                             dtype=torch.uint8, device=device)
-            _lib.check(lib.cce_backward(
-                g.data_ptr(), h2.data_ptr(), w2.data_ptr(), lab.data_ptr(), int(lab.dtype == torch.int64),
-                b32.data_ptr() if b32 is not None else None, lse.data_ptr(), n_valid.data_ptr(),
-                N, d, V, ignore_index, eps, zw, red, chunk_size,
-                dh.data_ptr() if dh is not None else None,
-                _lib.CCE_DTYPE_BF16 if (dh is not None and dh.dtype == torch.bfloat16) else _lib.CCE_DTYPE_F32,
-                dw.data_ptr() if dw is not None else None,
-                _lib.CCE_DTYPE_BF16 if (dw is not None and dw.dtype == torch.bfloat16) else _lib.CCE_DTYPE_F32,
-                db.data_ptr() if db is not None else None,
-                ws.data_ptr(), ws.numel(), _stream_handle(device)))
-        if dh is not None:
-            dh = dh.view(hshape).to(hdtype)
-        if dw is not None:
-            dw = dw.to(wdtype)
-        if db is not None:
-            db = db.to(bdtype)
+        # bf16 inputs get bf16 gradients; fp16 / fp32 inputs get them from fp32
+        dh, dw, db = torch.ops.chronicals_hip.cce_bwd(
+            grad_output, h2, w2, lab, lse, n_valid, b32, ignore_index, eps, zw, red, chunk_size,
+            need_dh, need_dw, need_db, hdtype != torch.bfloat16, wdtype != torch.bfloat16)
+        dh = dh.view(hshape).to(hdtype) if need_dh else None
+        dw = dw.to(wdtype) if need_dw else None
+        db = db.to(bdtype) if need_db else None
         return dh, dw, None, db, None, None, None, None, None
 
 

@@ -226,3 +226,47 @@ def test_full_size_vs_torch_fp32(gpu, name):
     assert_loss_close(got["loss"], ref["loss"].cpu().numpy(), f"{name} loss")
     assert_grad_close(got["dh"], ref["dh"].cpu().numpy(), f"{name} dh")
     assert_grad_close(got["dw"], ref["dw"].cpu().numpy(), f"{name} dw")
+
+
+def test_custom_ops_opcheck(gpu):
+    """chronicals_hip::cce_fwd / cce_bwd: schema (no input mutation or aliasing) and fake-tensor
+    implementations agree with the real kernels."""
+    import chronicals_amd.ops  # noqa: F401
+    h, w, lab, b = _rand_case(200, 64, 900, seed=41, bias=True)
+    hd = h.to(gpu, torch.bfloat16).contiguous()
+    wd = w.to(gpu, torch.bfloat16).contiguous()
+    ld = lab.to(gpu)
+    bd = b.to(gpu, torch.float32)
+    checks = ("test_schema", "test_faketensor")
+    for red in (0, 1, 2):
+        torch.library.opcheck(torch.ops.chronicals_hip.cce_fwd.default, (hd, wd, ld, bd, IGNORE, 0.1, 1e-4, red),
+                              test_utils=checks)
+    loss, lse, nv = torch.ops.chronicals_hip.cce_fwd(hd, wd, ld, bd, IGNORE, 0.0, 0.0, 1)
+    g = torch.tensor(1.0, device=gpu)
+    for need in ((True, True, True), (False, True, False), (True, False, True)):
+        torch.library.opcheck(torch.ops.chronicals_hip.cce_bwd.default,
+                              (g, hd, wd, ld, lse, nv, bd, IGNORE, 0.0, 0.0, 1, 512, *need, False, True),
+                              test_utils=checks)
+
+
+def test_torch_compile_fullgraph_matches_eager(gpu):
+    """The op traces into one graph (torch.compile, fullgraph) and gives the eager results."""
+    from chronicals_amd.kernels.cut_cross_entropy import cut_cross_entropy
+    h, w, lab, b = _rand_case(300, 128, 2000, seed=43, bias=True)
+
+    def loss_fn(hd, wd, ld, bd):
+        return cut_cross_entropy(hd, wd, ld, bd, 512, IGNORE, 0.1, 1e-4)
+
+    def run(fn):
+        hd = h.to(gpu, torch.bfloat16).requires_grad_(True)
+        wd = w.to(gpu, torch.bfloat16).requires_grad_(True)
+        bd = b.to(gpu, torch.float32).requires_grad_(True)
+        loss = fn(hd, wd, lab.to(gpu), bd)
+        loss.backward()  # the compiled graph's backward runs chronicals_hip::cce_bwd
+        torch.cuda.synchronize()
+        return loss.detach(), hd.grad, wd.grad, bd.grad
+
+    eager = run(loss_fn)
+    compiled = run(torch.compile(loss_fn, backend="aot_eager", fullgraph=True))
+    for a, c, name in zip(eager, compiled, ("loss", "dh", "dw", "db")):
+        assert torch.equal(a, c), name

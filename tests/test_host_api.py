@@ -83,3 +83,56 @@ def test_package_does_not_import_oracle():
         text = py.read_text()
         for pat in ("import oracle", "from oracle", "cce_oracle"):
             assert pat not in text, f"{py} reaches the oracle ({pat})"
+
+
+# ---------------------------------------------------------------------------
+# torch.library registration (chronicals_amd/ops.py)
+# ---------------------------------------------------------------------------
+
+def test_custom_ops_registered():
+    import chronicals_amd.ops  # noqa: F401
+    assert hasattr(torch.ops.chronicals_hip, "cce_fwd")
+    assert hasattr(torch.ops.chronicals_hip, "cce_bwd")
+
+
+@pytest.mark.parametrize("reduction,loss_shape", [(0, (300,)), (1, (1,)), (2, (1,))])
+def test_custom_op_fake_shapes_forward(reduction, loss_shape):
+    import chronicals_amd.ops  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        h = torch.empty(300, 128, dtype=torch.bfloat16, device="cuda")
+        w = torch.empty(1000, 128, dtype=torch.bfloat16, device="cuda")
+        lab = torch.empty(300, dtype=torch.int64, device="cuda")
+        loss, lse, nv = torch.ops.chronicals_hip.cce_fwd(h, w, lab, None, -100, 0.0, 0.0, reduction)
+        assert tuple(loss.shape) == loss_shape and loss.dtype == torch.float32
+        assert tuple(lse.shape) == (300,) and lse.dtype == torch.float32
+        assert tuple(nv.shape) == (1,) and nv.dtype == torch.int32
+
+
+@pytest.mark.parametrize("need", [(True, True, True), (True, False, False), (False, True, False), (False, False, True)])
+@pytest.mark.parametrize("f32", [False, True])
+def test_custom_op_fake_shapes_backward(need, f32):
+    import chronicals_amd.ops  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    need_dh, need_dw, need_db = need
+    with FakeTensorMode():
+        h = torch.empty(300, 128, dtype=torch.bfloat16, device="cuda")
+        w = torch.empty(1000, 128, dtype=torch.bfloat16, device="cuda")
+        lab = torch.empty(300, dtype=torch.int64, device="cuda")
+        b = torch.empty(1000, dtype=torch.float32, device="cuda")
+        lse = torch.empty(300, dtype=torch.float32, device="cuda")
+        nv = torch.empty(1, dtype=torch.int32, device="cuda")
+        g = torch.empty((), dtype=torch.float32, device="cuda")
+        dh, dw, db = torch.ops.chronicals_hip.cce_bwd(g, h, w, lab, lse, nv, b, -100, 0.0, 0.0, 1, 8192,
+                                                      need_dh, need_dw, need_db, f32, f32)
+        gd = torch.float32 if f32 else torch.bfloat16
+        assert tuple(dh.shape) == ((300, 128) if need_dh else (0,)) and dh.dtype == gd
+        assert tuple(dw.shape) == ((1000, 128) if need_dw else (0,)) and dw.dtype == gd
+        assert tuple(db.shape) == ((1000,) if need_db else (0,)) and db.dtype == torch.float32
+
+
+def test_custom_op_has_no_cpu_kernel():
+    import chronicals_amd.ops  # noqa: F401
+    with pytest.raises(NotImplementedError):
+        torch.ops.chronicals_hip.cce_fwd(torch.zeros(4, 8, dtype=torch.bfloat16), torch.zeros(5, 8, dtype=torch.bfloat16),
+                                         torch.zeros(4, dtype=torch.int64), None, -100, 0.0, 0.0, 1)
