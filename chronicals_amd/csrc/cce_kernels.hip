@@ -752,17 +752,17 @@ struct EpiAcc {
 // LDS elements of the pipeline stages: unpadded for the direct-to-LDS
 // pipelines, kPitch-padded rows for the register-staged ones.
 template <int BN>
-constexpr int gemm_lds_elems(int pipe) {
-  return 2 * (kBM + BN) * (pipe >= 4 ? 64 : kPitch);
+constexpr int gemm_lds_elems(int pipe, int nst = 2) {
+  return (pipe >= 4 ? nst : 2) * (kBM + BN) * (pipe >= 4 ? 64 : kPitch);
 }
 
-template <int BN, int W, bool AK, bool BKM, template <int, int> class EpiT, int PIPE>
+template <int BN, int W, bool AK, bool BKM, template <int, int> class EpiT, int PIPE, int NST = 2>
 __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename EpiT<BN, W>::Params& ep, int bid,
                                           int nb, bf16_t* smem) {
   typedef EpiT<BN, W> Epi;
   constexpr int kStage = (kBM + BN) * kPitch;
   // epilogue staging area, past the pipeline's LDS stages
-  bf16_t* const scratch = smem + gemm_lds_elems<BN>(PIPE);
+  bf16_t* const scratch = smem + gemm_lds_elems<BN>(PIPE, NST);
 
   const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
   const int wm = w >> 1, wn = w & 1;
@@ -797,8 +797,9 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
     static_assert(BKM && (PIPE == 5 || AK), "direct-to-LDS operand layouts");
     static_assert(PIPE == 4 || (!AK && BN <= 256), "PIPE 5 reads an MN-major A");
     constexpr int kSt = (kBM + BN) * 64;  // unpadded stage
-    bf16_t* const T0 = smem;
-    bf16_t* const T1 = smem + kSt;
+    static_assert(NST >= 2 && NST <= 3, "LDS holds two or three stages");
+    // DMA wave instructions per wave per slab
+    constexpr int kD = (PIPE == 4 ? kBM / (8 * W) : 32 / W) + BN / (8 * W);
     auto frags = [&](const bf16_t* Sc, int kk, Frags<BN, W>& f) {
       if constexpr (PIPE == 4)
         read_frags_swz<BN, W>(Sc, Sc + kBM * 64, kk, f, wm, wn, l);
@@ -819,17 +820,21 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
       }
     };
     // The DMA's LDS writes count on vmcnt; the barrier's own fence does not
-    // reliably wait for them, so each barrier that publishes a slab is
-    // preceded by an explicit vmcnt(0).  sched_barrier fences keep the MFMAs
-    // on their side of it.
-    // At the first barrier of a tile the previous tile's epilogue stores
-    // (issued after this slab's DMA; vector memory operations retire in
-    // issue order) may stay in flight: they drain behind the MFMAs instead of
-    // stalling the workgroup.
-    auto publish = [&](bool after_epilogue) {
+    // reliably wait for them, so each barrier B_s that publishes slab s+1 is
+    // preceded by an explicit wait.  Vector memory operations retire in
+    // issue order, so B_s may leave in flight exactly what was issued after
+    // slab s+1's DMA: the DMAs of slabs s+2 .. s+NST-1, and the previous
+    // tile's epilogue stores for the first NST-1 slabs of a tile (they then
+    // drain behind the MFMAs).  Near the end of the run, where some of those
+    // DMAs were never issued, it waits for everything.  sched_barrier fences
+    // keep the MFMAs on their side of the barrier.
+    auto publish = [&](int s_, bool after_epilogue) {
       __builtin_amdgcn_sched_barrier(0);
-      if (Epi::kStores > 0 && after_epilogue)
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(Epi::kStores));
+      const bool deep = s_ + NST - 1 < ((t1 - t0) * KT);
+      if (deep && Epi::kStores > 0 && after_epilogue)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * kD + Epi::kStores));
+      else if (deep && NST > 2)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * kD));
       else
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
@@ -843,17 +848,28 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
       __builtin_amdgcn_sched_group_barrier(0x008, WaveCfg<W>::kFM * (BN / 64), 0);
     };
     const int total = (t1 - t0) * KT;
-    issue(T0);
-    if (total > 1) issue(T1);
-    publish(false);
+    // prologue: slabs 0 .. NST-1 in flight, wait for slab 0
+    issue(smem);
+    if (total > 1) issue(smem + kSt);
+    if constexpr (NST == 3) {
+      if (total > 2) issue(smem + 2 * kSt);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (NST == 3 && total > 2)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kD));
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
     Frags<BN, W> fa, fb;
-    frags(T0, 0, fa);
-    int s = 0;
+    frags(smem, 0, fa);
+    int s = 0, cur = 0;  // cur = s % NST
     for (int tn = t0; tn < t1; ++tn) {
       acc.zero();
       for (int kt = 0; kt < KT; ++kt, ++s) {
-        bf16_t* const Sc = (s & 1) ? T1 : T0;
-        bf16_t* const Sn = (s & 1) ? T0 : T1;
+        const int nxt = (cur + 1 == NST) ? 0 : cur + 1;
+        bf16_t* const Sc = smem + cur * kSt;
+        bf16_t* const Sn = smem + nxt * kSt;
         frags(Sc, 1, fb);
         mfma_frags<BN, W>(fa, acc);
         order();
@@ -863,12 +879,13 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
         frags(Sc, 3, fb);
         mfma_frags<BN, W>(fa, acc);
         order();
-        publish(kt == 0 && tn != t0);  // B_s
+        publish(s, kt <= NST - 2 && tn != t0);  // B_s
         frags(Sn, 0, fa);  // past the last slab this reads stale data, unused
         mfma_frags<BN, W>(fb, acc);
         order();
         __builtin_amdgcn_sched_barrier(0);
-        if (s + 2 < total) issue(Sc);
+        if (s + NST < total) issue(Sc);  // stage of slab s is free after B_s
+        cur = nxt;
       }
       Epi::tile(ep, st, acc, g, tm, tn, wm, wn, l, scratch);
     }
@@ -993,10 +1010,10 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
   Epi::finish(ep, st, g, tm, split, smem, wm, wn, l);
 }
 
-template <int BN, int W, bool AK, bool BKM, template <int, int> class EpiT, int PIPE>
+template <int BN, int W, bool AK, bool BKM, template <int, int> class EpiT, int PIPE, int NST = 2>
 __global__ __launch_bounds__(W * 64) void gemm_kernel(GemmShape g, typename EpiT<BN, W>::Params ep) {
-  __shared__ __attribute__((aligned(16))) bf16_t smem[gemm_lds_elems<BN>(PIPE) + EpiT<BN, W>::kScratch];
-  gemm_body<BN, W, AK, BKM, EpiT, PIPE>(g, ep, blockIdx.x, gridDim.x, smem);
+  __shared__ __attribute__((aligned(16))) bf16_t smem[gemm_lds_elems<BN>(PIPE, NST) + EpiT<BN, W>::kScratch];
+  gemm_body<BN, W, AK, BKM, EpiT, PIPE, NST>(g, ep, blockIdx.x, gridDim.x, smem);
 }
 
 // dW and dH GEMMs of one vocabulary band in a single launch.  The first
@@ -1021,7 +1038,8 @@ __global__ __launch_bounds__(W * 64) void dual_acc_kernel(GemmShape g_dw, AccPar
 // on padding, and the wide tiles do the most work per CU-second).
 // Workgroups are numbered longest first — dW (K = N), dH (K = band width),
 // then the short recompute tiles, which fill the CUs the long tiles leave
-// idle at the end of the band.
+// idle at the end of the band.  The 128-wide tail tiles fit three LDS stages
+// (two slabs in flight) in the space the 256-wide tiles use for two.
 struct BandLaunch {
   GemmShape dw;
   AccParams e_dw;
@@ -1046,7 +1064,7 @@ __global__ __launch_bounds__(kWarp8 * 64) void band_kernel(BandLaunch p) {
   }
   b -= p.nb_dw;
   if (b < p.nb_dw2) {
-    gemm_body<kSlowBN, kWarp8, false, true, EpiAcc, 5>(p.dw2, p.e_dw2, b, p.nb_dw2, smem);
+    gemm_body<kSlowBN, kWarp8, false, true, EpiAcc, 5, 3>(p.dw2, p.e_dw2, b, p.nb_dw2, smem);
     return;
   }
   b -= p.nb_dw2;
@@ -1056,7 +1074,7 @@ __global__ __launch_bounds__(kWarp8 * 64) void band_kernel(BandLaunch p) {
   }
   b -= p.nb_dh;
   if (b < p.nb_dh2) {
-    gemm_body<kSlowBN, kWarp8, true, true, EpiAcc, 4>(p.dh2, p.e_dh2, b, p.nb_dh2, smem);
+    gemm_body<kSlowBN, kWarp8, true, true, EpiAcc, 4, 3>(p.dh2, p.e_dh2, b, p.nb_dh2, smem);
     return;
   }
   b -= p.nb_dh2;
@@ -1437,13 +1455,13 @@ double gemm_flops(long M, long N, long K) { return 2.0 * (double)M * (double)N *
 
 // A GEMM launch; `credited` is the algorithmic share of its FLOPs (the
 // logits recompute of the backward is executed but not credited).
-template <int BN, int W, bool AK, bool BK, template <int, int> class EpiT, int PIPE = 3>
+template <int BN, int W, bool AK, bool BK, template <int, int> class EpiT, int PIPE = 3, int NST = 2>
 int launch_gemm(const GemmShape& g, const typename EpiT<BN, W>::Params& ep, int nblocks, hipStream_t st,
                 int kind, bool credited) {
   if (nblocks <= 0) return CCE_OK;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   const bool timed = timing_begin(st, &e0, &e1);
-  hipLaunchKernelGGL((gemm_kernel<BN, W, AK, BK, EpiT, PIPE>), dim3(nblocks), dim3(W * 64), 0, st, g, ep);
+  hipLaunchKernelGGL((gemm_kernel<BN, W, AK, BK, EpiT, PIPE, NST>), dim3(nblocks), dim3(W * 64), 0, st, g, ep);
   HIP_TRY(hipGetLastError());
   if (timed) {
     const double f = gemm_flops(g.M, g.N, g.K);
