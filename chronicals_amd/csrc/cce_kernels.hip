@@ -1342,8 +1342,12 @@ int forward_splits(long N, long d, long V) {
   return (int)s;
 }
 
+// Vocabulary band width: chunk rounded up to a multiple of 256, within
+// [256, V rounded up] and at most 2^20 columns (a band's 256-row operand
+// tiles then stay inside one buffer descriptor's 2 GB range).
+constexpr long kMaxBand = 1L << 20;
 long band_width(long V, long chunk) {
-  long vb = chunk <= 0 ? 8192 : chunk;
+  long vb = chunk <= 0 ? 8192 : (chunk > kMaxBand ? kMaxBand : chunk);
   vb = align_up((size_t)vb, 256);
   const long vmax = (long)align_up((size_t)V, 256);
   if (vb > vmax) vb = vmax;
@@ -1403,12 +1407,17 @@ BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bo
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
 
+constexpr long kMaxRows = 1L << 21;  // tokens per call
+
 int check_dims(long N, long d, long V) {
   if (N < 0) return fail(CCE_ERR_INVALID_ARG, "N must be >= 0 (got %ld)", N);
   if (d <= 0 || d % 8 != 0) return fail(CCE_ERR_INVALID_ARG, "hidden dim d must be a positive multiple of 8 (got %ld)", d);
   if (V <= 0) return fail(CCE_ERR_INVALID_ARG, "vocab size V must be > 0 (got %ld)", V);
-  if (N > (1L << 30) || V > (1L << 30) || d > (1L << 20))
-    return fail(CCE_ERR_INVALID_ARG, "problem too large (N=%ld d=%ld V=%ld)", N, d, V);
+  // N: the dW GEMM reads 256-row tiles of H^T ([d][N]) through one buffer
+  // descriptor, whose range (2 GB) and 32-bit lane offsets bound 256*N*2 bytes
+  if (N > kMaxRows || V > (1L << 30) || d > (1L << 20))
+    return fail(CCE_ERR_INVALID_ARG, "problem too large (N=%ld d=%ld V=%ld; limits N <= %ld, V <= 2^30, d <= 2^20)",
+                N, d, V, kMaxRows);
   return CCE_OK;
 }
 

@@ -14,6 +14,8 @@
  * Conventions
  *   - hidden  [N][d] and weight [V][d] are row-major bf16 (raw 16-bit words),
  *     16-byte aligned, d a multiple of 8.  All arithmetic accumulates in fp32.
+ *   - Limits: N <= 2^21 tokens per call, V <= 2^30, d <= 2^20; larger
+ *     problems return CCE_ERR_INVALID_ARG.  chunk_size above 2^20 is clamped.
  *   - labels [N] are int64 (labels_int64 = 1) or int32 (labels_int64 = 0).
  *     A row whose label equals ignore_index contributes nothing; a label
  *     outside [0, V) that is not ignore_index has no target logit (loss = lse),

@@ -104,8 +104,11 @@ def test_workspace_queries(lib):
     assert _lib.forward_workspace_bytes(0, 64, 300, _lib.CCE_REDUCTION_MEAN) > 0
     assert _lib.forward_workspace_bytes(0, 64, 300, _lib.CCE_REDUCTION_NONE) > 0
     assert _lib.backward_workspace_bytes(0, 64, 300, 8192, True, True) >= 0
-    # chunk_size bounds the band
+    # chunk_size bounds the band; bands wider than 2^20 columns are clamped
     assert _lib.backward_workspace_bytes(16384, 896, 151936, 2048, True, True) < b
+    assert (_lib.backward_workspace_bytes(64, 64, 2 ** 22, 2 ** 22, True, True)
+            == _lib.backward_workspace_bytes(64, 64, 2 ** 22, 2 ** 20, True, True))
+    assert _lib.forward_workspace_bytes(2 ** 21, 64, 1000, _lib.CCE_REDUCTION_MEAN) > 0  # the largest N
 
 
 @pytest.mark.parametrize("N,d,V,red,msg", [
@@ -114,6 +117,9 @@ def test_workspace_queries(lib):
     (16, 64, 0, 1, "vocab"),
     (-1, 64, 10, 1, "N must be"),
     (16, 64, 100, 5, "reduction"),
+    (2 ** 21 + 1, 64, 100, 1, "too large"),   # tokens per call
+    (16, 2 ** 20 + 8, 100, 1, "too large"),
+    (16, 64, 2 ** 30 + 1, 1, "too large"),
 ])
 def test_workspace_query_rejects_bad_arguments(lib, N, d, V, red, msg):
     out = ctypes.c_size_t(0)
