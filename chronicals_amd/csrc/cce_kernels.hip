@@ -78,9 +78,12 @@ __device__ inline f32x16 mfma_32x32x16(u32x4 a, u32x4 b, f32x16 c) {
                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// Two floats -> packed bf16 pair (round to nearest even): one
+// v_cvt_pk_bf16_f32 on gfx950.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ inline uint32_t pack_bf16x2(float lo, float hi) {
-  const __bf16 a = (__bf16)lo, b = (__bf16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 
 __device__ inline float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
@@ -607,6 +610,9 @@ struct EpiGradT {
     // this row tile of G: rows past M are out of the descriptor's range
     const int rows = min(g.M - tm * kBM, kBM);
     const __amdgpu_buffer_rsrc_t gr = make_rsrc(p.G + (long)tm * kBM * p.ldg, (long)rows * p.ldg * 2);
+    // interior tile without bias: every column is inside the band and rows
+    // past M are dropped by the store descriptor, so no per-element checks
+    const bool interior = !HB && (tn + 1) * BN <= g.N;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int m = tm * kBM + acc_row<W>(wm, i, l);
@@ -621,29 +627,55 @@ struct EpiGradT {
       }
 #pragma unroll
       for (int jp = 0; jp < FN / 2; ++jp) {
+        // G without the one-hot term, packed to bf16 into the staging block;
+        // the 8-byte piece hc (of 16 per 128-byte row) lives at hc ^ (row & 15)
+        auto stage = [&](int jj, int q, const float (&gv)[4]) {
+          const int hc = (jj * 8 + 2 * q + (l >> 5)) ^ (r & 15);
+          *reinterpret_cast<u32x2*>(ws + r * 64 + hc * 4) =
+              u32x2{pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3])};
+        };
+        if (interior) {
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
+          for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int cb = tn * BN + acc_col<BN>(wn, 2 * jp + jj, q, l);
-            float gv[4];
+            for (int q = 0; q < 4; ++q) {
+              float gv[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int col = cb + e;
-              float gg = 0.f;
-              if (mok && col < g.N) {
-                const float b = HB ? p.bias[p.v0 + col] : 0.f;
-                const float x = (acc.v[i][2 * jp + jj][4 * q + e] + b) * kLog2e - rp.x;
-                gg = rp.y * fast_exp2(x) - rp.w;
-                if (col == lab) gg -= rp.z;
-              }
-              gv[e] = gg;
+              for (int e = 0; e < 4; ++e)
+                gv[e] = __builtin_fmaf(rp.y, fast_exp2(__builtin_fmaf(acc.v[i][2 * jp + jj][4 * q + e], kLog2e, -rp.x)),
+                                       -rp.w);
+              stage(jj, q, gv);
             }
-            // 8-byte piece hc (of 16 per 128-byte row) lives at hc ^ (row & 15)
-            const int hc = (jj * 8 + 2 * q + (l >> 5)) ^ (r & 15);
-            *reinterpret_cast<u32x2*>(ws + r * 64 + hc * 4) =
-                u32x2{pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3])};
-          }
+        } else {
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int cb = tn * BN + acc_col<BN>(wn, 2 * jp + jj, q, l);
+              float gv[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int col = cb + e;
+                float gg = 0.f;
+                if (mok && col < g.N) {
+                  const float b = HB ? p.bias[p.v0 + col] : 0.f;
+                  gg = rp.y * fast_exp2((acc.v[i][2 * jp + jj][4 * q + e] + b) * kLog2e - rp.x) - rp.w;
+                }
+                gv[e] = gg;
+              }
+              stage(jj, q, gv);
+            }
+        }
+        asm volatile("" ::: "memory");
+        // the one-hot term: the target column of row r, if it falls in this
+        // 64-column block, is corrected in place by the row's first lane
+        // (labels outside the band are negative or past it and never match)
+        const unsigned lc = (unsigned)(lab - (tn * BN + wn * (BN / 2) + jp * 64));
+        if (l < 32 && lc < 64u) {
+          bf16_t* const t = ws + r * 64 + ((((int)lc >> 2) ^ (r & 15)) << 2) + (lc & 3);
+          const float v = bf16_to_f32(*t) - rp.z;
+          *t = __builtin_bit_cast(bf16_t, (__bf16)v);
+        }
         asm volatile("" ::: "memory");
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
