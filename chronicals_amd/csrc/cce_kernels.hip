@@ -688,6 +688,7 @@ struct EpiGradT {
           __builtin_amdgcn_raw_buffer_store_b128(v, gr, (int)(((long)trow * p.ldg + gcol) * 2), 0, 0);
         }
         asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);  // one 64-column block live at a time
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -886,9 +887,11 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
     if constexpr (NST == 3) {
       if (total > 2) issue(smem + 2 * kSt);
     }
+    // wait for slab 0 only: after its DMA come those of slabs 1 .. NST-1
+    // (all issued when total > NST)
     __builtin_amdgcn_sched_barrier(0);
-    if (NST == 3 && total > 2)
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kD));
+    if (total > NST)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NST - 1) * kD) : "memory");
     else
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -912,7 +915,9 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
         mfma_frags<BN, W>(fa, acc);
         order();
         publish(s, kt <= NST - 2 && tn != t0);  // B_s
-        frags(Sn, 0, fa);  // past the last slab this reads stale data, unused
+        // the next tile's first fragments are read after this tile's
+        // epilogue, so they are not live (24 VGPRs) while it runs
+        if (kt + 1 < KT) frags(Sn, 0, fa);
         mfma_frags<BN, W>(fb, acc);
         order();
         __builtin_amdgcn_sched_barrier(0);
@@ -920,6 +925,7 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g, const typename Epi
         cur = nxt;
       }
       Epi::tile(ep, st, acc, g, tm, tn, wm, wn, l, scratch);
+      if (tn + 1 < t1) frags(smem + cur * kSt, 0, fa);  // slab s+1, published at B_s
     }
     Epi::finish(ep, st, g, tm, split, smem, wm, wn, l);
     return;
