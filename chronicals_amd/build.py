@@ -17,6 +17,8 @@ SRC = os.path.join(PKG_DIR, "csrc", "cce_kernels.hip")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_NAME = "libchronicals_cce.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
+# per-kernel register / LDS / spill report of the last build (compiler remarks)
+RESOURCES_PATH = os.path.join(LIB_DIR, "libchronicals_cce.resources.txt")
 ARCH = "gfx950"
 
 
@@ -38,9 +40,30 @@ def compile_command(out_path: str) -> list:
         # packed fp32 VALU ops stay off (the compiler may not form them)
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-I", os.path.join(REPO_DIR, "include"),
+        # per-kernel resource usage (VGPRs, spills, LDS) as compiler remarks
+        "-Rpass-analysis=kernel-resource-usage",
         "-o", out_path,
         SRC,
     ]
+
+
+def parse_resources(text: str) -> dict:
+    """{kernel symbol: {field: int}} from kernel-resource-usage remarks."""
+    out, cur = {}, None
+    for line in text.splitlines():
+        if "remark:" not in line:
+            continue
+        body = line.split("remark:", 1)[1].strip()
+        body = body.split(" [-Rpass", 1)[0]
+        if body.startswith("Function Name:"):
+            cur = out.setdefault(body.split(":", 1)[1].strip(), {})
+        elif cur is not None and ":" in body:
+            key, val = body.split(":", 1)
+            try:
+                cur[key.strip()] = int(val.strip().split()[0])
+            except ValueError:
+                pass
+    return out
 
 
 def build(verbose: bool = False) -> str:
@@ -55,6 +78,13 @@ def build(verbose: bool = False) -> str:
         sys.stderr.write(proc.stdout + proc.stderr)
         raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
     os.replace(tmp, LIB_PATH)
+    res = parse_resources(proc.stdout + proc.stderr)
+    with open(RESOURCES_PATH, "w") as f:
+        for name in sorted(res):
+            f.write(name + " " + " ".join(f"{k.replace(' ', '_')}={v}" for k, v in sorted(res[name].items())) + "\n")
+    spills = {n: r.get("VGPRs Spill", 0) for n, r in res.items() if r.get("VGPRs Spill", 0)}
+    if spills:
+        sys.stderr.write(f"warning: kernels spill VGPRs to scratch: {spills}\n")
     return LIB_PATH
 
 

@@ -162,3 +162,21 @@ def test_build_command_targets_gfx950():
     cmd = _build.compile_command("/tmp/x.so")
     assert "--offload-arch=gfx950" in cmd
     assert "-packed-fp32-ops" in cmd
+
+
+def test_built_kernels_do_not_spill():
+    """The build records each kernel's compiler resource report: no kernel may spill VGPRs to
+    scratch (a spill reload inside the pipeline would also wait on the outstanding slab DMA), and
+    every kernel fits the 160 KB of LDS a workgroup can have."""
+    from chronicals_amd import build as _build
+    if not os.path.exists(_build.RESOURCES_PATH):
+        pytest.skip("library not built in this tree")
+    kernels = {}
+    with open(_build.RESOURCES_PATH) as f:
+        for line in f:
+            name, *fields = line.split()
+            kernels[name] = dict(kv.split("=", 1) for kv in fields)
+    assert any("band_kernel" in n for n in kernels) and any("gemm_kernel" in n for n in kernels)
+    for name, r in kernels.items():
+        assert int(r.get("VGPRs_Spill", 0)) == 0, f"{name} spills {r['VGPRs_Spill']} VGPRs"
+        assert int(r.get("LDS_Size_[bytes/block]", 0)) <= 160 * 1024, name
