@@ -11,7 +11,7 @@ import threading
 from . import build as _build
 
 # constants mirrored from include/chronicals_cce.h
-CCE_ABI_VERSION = 2
+CCE_ABI_VERSION = 3
 CCE_OK = 0
 CCE_ERR_INVALID_ARG = 1
 CCE_ERR_WORKSPACE = 2
@@ -21,6 +21,9 @@ CCE_REDUCTION_MEAN = 1
 CCE_REDUCTION_SUM = 2
 CCE_DTYPE_BF16 = 0
 CCE_DTYPE_F32 = 1
+CCE_DTYPE_F16 = 2
+CCE_SMOOTH_LOGV = 0
+CCE_SMOOTH_UNIFORM = 1
 
 CCE_KERNEL_FWD_LSE = 0
 CCE_KERNEL_BWD_GRAD = 1
@@ -28,9 +31,12 @@ CCE_KERNEL_BWD_DH = 2
 CCE_KERNEL_BWD_DW = 3
 CCE_KERNEL_BWD_DHDW = 4
 CCE_KERNEL_BWD_BAND = 5
-CCE_KERNEL_KINDS = 6
+CCE_KERNEL_LOGITS_FWD = 6
+CCE_KERNEL_LOGITS_BWD = 7
+CCE_KERNEL_KINDS = 8
 KERNEL_KIND_NAMES = {CCE_KERNEL_FWD_LSE: "fwd_lse", CCE_KERNEL_BWD_GRAD: "bwd_grad", CCE_KERNEL_BWD_DH: "bwd_dh",
-                     CCE_KERNEL_BWD_DW: "bwd_dw", CCE_KERNEL_BWD_DHDW: "bwd_dhdw", CCE_KERNEL_BWD_BAND: "bwd_band"}
+                     CCE_KERNEL_BWD_DW: "bwd_dw", CCE_KERNEL_BWD_DHDW: "bwd_dhdw", CCE_KERNEL_BWD_BAND: "bwd_band",
+                     CCE_KERNEL_LOGITS_FWD: "logits_fwd", CCE_KERNEL_LOGITS_BWD: "logits_bwd"}
 
 REDUCTIONS = {"none": CCE_REDUCTION_NONE, "mean": CCE_REDUCTION_MEAN, "sum": CCE_REDUCTION_SUM}
 
@@ -60,6 +66,20 @@ SIGNATURES = {
         _f32, _f32, _i32, _i64,              # label_smoothing, z_loss_weight, reduction, chunk_size
         _vp, _i32, _vp, _i32, _vp,           # grad_hidden, dtype, grad_weight, dtype, grad_bias
         _vp, _sz, _vp,                       # workspace, workspace_bytes, stream
+    ]),
+    "cce_logits_forward_workspace_bytes": (_i32, [_i64, _i64, _i32, ctypes.POINTER(_sz)]),
+    "cce_logits_forward": (_i32, [
+        _vp, _i32, _i64, _vp, _i32,          # logits, dtype, ld, labels, labels_int64
+        _i64, _i64, _i64,                    # N, V, ignore_index
+        _f32, _f32, _i32, _i32,              # label_smoothing, z_loss_weight, smoothing_form, reduction
+        _vp, _vp, _vp,                       # loss_out, lse_out, n_valid_out
+        _vp, _sz, _vp,                       # workspace, workspace_bytes, stream
+    ]),
+    "cce_logits_backward": (_i32, [
+        _vp, _vp, _i32, _i64, _vp, _i32,     # grad_out, logits, dtype, ld, labels, labels_int64
+        _vp, _vp, _i64, _i64, _i64,          # lse, n_valid, N, V, ignore_index
+        _f32, _f32, _i32, _i32,              # label_smoothing, z_loss_weight, smoothing_form, reduction
+        _vp, _i32, _i64, _vp,                # grad_logits, grad_dtype, ld_grad, stream
     ]),
     "cce_kernel_timing_enable": (_i32, [_i32]),
     "cce_kernel_timing_read": (_i32, [_i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64),
@@ -119,6 +139,12 @@ def forward_workspace_bytes(N: int, d: int, V: int, reduction: int) -> int:
 def backward_workspace_bytes(N: int, d: int, V: int, chunk_size: int, need_dh: bool, need_dw: bool) -> int:
     out = _sz(0)
     check(load().cce_backward_workspace_bytes(N, d, V, chunk_size, int(need_dh), int(need_dw), ctypes.byref(out)))
+    return out.value
+
+
+def logits_forward_workspace_bytes(N: int, V: int, reduction: int) -> int:
+    out = _sz(0)
+    check(load().cce_logits_forward_workspace_bytes(N, V, reduction, ctypes.byref(out)))
     return out.value
 
 

@@ -1235,6 +1235,223 @@ __global__ __launch_bounds__(1024) void fwd_finalize_kernel(const float* __restr
   }
 }
 
+// ---------------------------------------------------------------------------
+// Cross-entropy over logits that already exist (row kernels, HBM-bound).
+// One 256-thread workgroup streams one row of X [N][ld] (bf16, fp16 or fp32)
+// with 16-byte loads; a row whose start is not 16-byte aligned (e.g. odd V in
+// bf16) takes its head and tail elements one by one.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ inline float elem_to_f32(T v);
+template <>
+__device__ inline float elem_to_f32<float>(float v) { return v; }
+template <>
+__device__ inline float elem_to_f32<_Float16>(_Float16 v) { return (float)v; }
+template <>
+__device__ inline float elem_to_f32<uint16_t>(uint16_t v) { return bf16_to_f32(v); }
+
+template <typename T>
+__device__ inline T f32_to_elem(float v);
+template <>
+__device__ inline float f32_to_elem<float>(float v) { return v; }
+template <>
+__device__ inline _Float16 f32_to_elem<_Float16>(float v) { return (_Float16)v; }
+template <>
+__device__ inline uint16_t f32_to_elem<uint16_t>(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
+
+// Split of row [0, V) at address p into a scalar head, 16-byte chunks and a
+// scalar tail.
+template <typename T>
+struct RowSplit {
+  static constexpr int E = 16 / sizeof(T);
+  int head, chunks, tail_start;
+  __device__ RowSplit(const T* p, int V) {
+    const int mis = (int)((reinterpret_cast<uintptr_t>(p) & 15u) / sizeof(T));
+    head = mis ? min(E - mis, V) : 0;
+    chunks = (V - head) / E;
+    tail_start = head + chunks * E;
+  }
+};
+
+// Calls f(c, chunk) for this thread's 16-byte chunks c = tid, tid + 256, ...
+// below `chunks`, issuing four loads before the first use so that every wave
+// keeps 4 KB of HBM reads in flight.
+template <typename F>
+__device__ __forceinline__ void for_each_chunk(const u32x4* __restrict__ body, int chunks, int tid, F&& f) {
+  constexpr int U = 4;
+  int c = tid;
+  for (; c + (U - 1) * 256 < chunks; c += U * 256) {
+    u32x4 raw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) raw[u] = __builtin_nontemporal_load(body + c + u * 256);
+#pragma unroll
+    for (int u = 0; u < U; ++u) f(c + u * 256, raw[u]);
+  }
+  for (; c < chunks; c += 256) f(c, __builtin_nontemporal_load(body + c));
+}
+
+// Workgroup-wide merge of base-2 (max, sum) pairs; every thread gets the result.
+__device__ inline void block_merge_ms(float& m, float& s, float* red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
+    const float mn = fmaxf(m, m2);
+    s = s * fast_exp2(m - mn) + s2 * fast_exp2(m2 - mn);
+    m = mn;
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red[2 * w] = m;
+    red[2 * w + 1] = s;
+  }
+  __syncthreads();
+  m = red[0];
+  s = red[1];
+#pragma unroll
+  for (int k = 1; k < 4; ++k) {
+    const float m2 = red[2 * k], s2 = red[2 * k + 1];
+    const float mn = fmaxf(m, m2);
+    s = s * fast_exp2(m - mn) + s2 * fast_exp2(m2 - mn);
+    m = mn;
+  }
+}
+
+// Workgroup-wide sum; every thread gets the result.
+__device__ inline float block_sum(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  __syncthreads();  // red may still be read by an earlier merge
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Forward: lse[n] = log sum exp(x), the row loss (0 for rows labelled
+// ignore_index; a label outside [0, V) has no target logit)
+//   CCE_SMOOTH_LOGV:    (1-eps)*(lse - x[label]) + eps*log(V)       + z*lse^2
+//   CCE_SMOOTH_UNIFORM: (1-eps)*(lse - x[label]) + eps*(lse - sum(x)/V) + z*lse^2
+// and one (sum, count) partial per row for fwd_finalize_kernel.
+template <typename T>
+__global__ __launch_bounds__(256) void ce_logits_fwd_kernel(const T* __restrict__ X, long ld, const void* labels,
+                                                            int labels64, int V, long ignore_index, float eps,
+                                                            float zw, float logV, int smooth_mode,
+                                                            float* __restrict__ lse_out,
+                                                            float* __restrict__ rowloss, float* __restrict__ bsum,
+                                                            int* __restrict__ bcnt) {
+  __shared__ float red[8];
+  const int n = blockIdx.x, tid = threadIdx.x;
+  const T* row = X + (long)n * ld;
+  const RowSplit<T> sp(row, V);
+  // the target logit is fetched first, so its latency hides under the stream
+  long lab = 0;
+  float t = 0.f;
+  if (tid == 0) {
+    lab = load_label(labels, labels64, n);
+    if (lab != ignore_index && lab >= 0 && lab < V) t = elem_to_f32(row[lab]);
+  }
+  float m = kNegBig, s = 0.f;  // base 2
+  float sx = 0.f;              // sum of x (natural units)
+  auto add1 = [&](float x) {
+    const float x2 = x * kLog2e, mn = fmaxf(m, x2);
+    s = s * fast_exp2(m - mn) + fast_exp2(x2 - mn);
+    m = mn;
+    sx += x;
+  };
+  if (tid < sp.head) add1(elem_to_f32(row[tid]));
+  if (tid < V - sp.tail_start) add1(elem_to_f32(row[sp.tail_start + tid]));
+  const u32x4* body = reinterpret_cast<const u32x4*>(row + sp.head);
+  for_each_chunk(body, sp.chunks, tid, [&](int, const u32x4& raw) {
+    const T* v = reinterpret_cast<const T*>(&raw);
+    float x[RowSplit<T>::E], mx = kNegBig, cs = 0.f;
+#pragma unroll
+    for (int e = 0; e < RowSplit<T>::E; ++e) {
+      const float xe = elem_to_f32(v[e]);
+      cs += xe;
+      x[e] = xe * kLog2e;
+      mx = fmaxf(mx, x[e]);
+    }
+    const float mn = fmaxf(m, mx);
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < RowSplit<T>::E; ++e) acc += fast_exp2(x[e] - mn);
+    s = s * fast_exp2(m - mn) + acc;
+    m = mn;
+    sx += cs;
+  });
+  block_merge_ms(m, s, red);
+  if (smooth_mode == CCE_SMOOTH_UNIFORM) sx = block_sum(sx, red);
+  if (tid == 0) {
+    const float lse = m * kLn2 + logf(s + 1e-10f);
+    const bool valid = lab != ignore_index;
+    const float smooth = smooth_mode == CCE_SMOOTH_UNIFORM ? lse - sx / (float)V : logV;
+    const float loss = valid ? (1.f - eps) * (lse - t) + eps * smooth + zw * lse * lse : 0.f;
+    lse_out[n] = lse;
+    rowloss[n] = loss;
+    bsum[n] = loss;
+    bcnt[n] = valid ? 1 : 0;
+  }
+}
+
+// Backward: the derivative of the forward's row loss, times g_n, for valid
+// rows (0 for ignored rows), with p_v = exp(x_v - lse):
+//   CCE_SMOOTH_LOGV:    g_n * (((1-eps) + 2z*lse) * p_v - (1-eps) * [v == label])
+//   CCE_SMOOTH_UNIFORM: g_n * ((1 + 2z*lse) * p_v - eps/V - (1-eps) * [v == label])
+// g_n = grad_out[n] ('none'), grad_out[0] ('sum') or grad_out[0] / max(n_valid, 1)
+// ('mean').  dX may be X itself (same dtype and stride): every element is read
+// and then written by the same thread.
+template <typename T, typename TO>
+__global__ __launch_bounds__(256) void ce_logits_bwd_kernel(const float* __restrict__ grad_out, const T* X, long ld,
+                                                            const void* labels, int labels64,
+                                                            const float* __restrict__ lse,
+                                                            const int32_t* __restrict__ n_valid, int V,
+                                                            long ignore_index, float eps, float zw, int smooth_mode,
+                                                            int reduction, TO* dX, long ldg) {
+  const int n = blockIdx.x, tid = threadIdx.x;
+  const T* row = X + (long)n * ld;
+  TO* drow = dX + (long)n * ldg;
+  const long lab = load_label(labels, labels64, n);
+  const bool valid = lab != ignore_index;
+  float g = reduction == CCE_REDUCTION_NONE ? grad_out[n] : grad_out[0];
+  if (reduction == CCE_REDUCTION_MEAN) g /= (float)(n_valid[0] > 1 ? n_valid[0] : 1);
+  const float l = lse[n];
+  const bool uni = smooth_mode == CCE_SMOOTH_UNIFORM;
+  const float cP = valid ? g * ((uni ? 1.f : 1.f - eps) + 2.f * zw * l) : 0.f;
+  const float cU = valid && uni ? g * eps / (float)V : 0.f;
+  const float cT = valid ? g * (1.f - eps) : 0.f;
+  const float l2 = l * kLog2e;
+  const long t = (valid && lab >= 0 && lab < V) ? lab : -1;
+  auto grad1 = [&](int v, float x) { return (cP * fast_exp2(x * kLog2e - l2) - cU) - (v == t ? cT : 0.f); };
+  const RowSplit<T> sp(row, V);
+  // 16-byte chunks of X map onto (sizeof(TO)/sizeof(T)) aligned 16-byte
+  // chunks of dX when dX's row is aligned like X's (the usual case);
+  // otherwise every element goes one by one
+  constexpr int E = RowSplit<T>::E;
+  constexpr int kOut = sizeof(TO) / sizeof(T);
+  static_assert(kOut * sizeof(T) == sizeof(TO), "output element size must be a multiple of the input's");
+  const bool vec = ((reinterpret_cast<uintptr_t>(drow + sp.head) & 15u) == 0);
+  if (!vec) {
+    for (int v = tid; v < V; v += 256) drow[v] = f32_to_elem<TO>(grad1(v, elem_to_f32(row[v])));
+    return;
+  }
+  if (tid < sp.head) drow[tid] = f32_to_elem<TO>(grad1(tid, elem_to_f32(row[tid])));
+  if (tid < V - sp.tail_start) {
+    const int v = sp.tail_start + tid;
+    drow[v] = f32_to_elem<TO>(grad1(v, elem_to_f32(row[v])));
+  }
+  const u32x4* body = reinterpret_cast<const u32x4*>(row + sp.head);
+  u32x4* dbody = reinterpret_cast<u32x4*>(drow + sp.head);
+  for_each_chunk(body, sp.chunks, tid, [&](int c, const u32x4& raw) {
+    const T* v = reinterpret_cast<const T*>(&raw);
+    u32x4 out[kOut];
+    TO* o = reinterpret_cast<TO*>(out);
+    const int v0 = sp.head + c * E;
+#pragma unroll
+    for (int e = 0; e < E; ++e) o[e] = f32_to_elem<TO>(grad1(v0 + e, elem_to_f32(v[e])));
+#pragma unroll
+    for (int k = 0; k < kOut; ++k) __builtin_nontemporal_store(out[k], dbody + c * kOut + k);
+  });
+}
+
 // Per-row backward coefficients.
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__ grad_out,
                                                        const float* __restrict__ lse,
@@ -1590,6 +1807,42 @@ int launch_band(const BandLaunch& p, bool has_bias, hipStream_t st) {
   return CCE_OK;
 }
 
+// Logits-in cross-entropy: dtype codes and workspace.
+int logits_elem_size(int dtype) {
+  return dtype == CCE_DTYPE_F32 ? 4 : (dtype == CCE_DTYPE_BF16 || dtype == CCE_DTYPE_F16) ? 2 : 0;
+}
+
+struct LogitsLayout {
+  float *rowloss, *bsum;
+  int* bcnt;
+  size_t bytes;
+};
+
+LogitsLayout logits_layout(void* ws, long N) {
+  Carver c(ws);
+  LogitsLayout L;
+  const size_t n = (size_t)(N > 0 ? N : 1);
+  L.rowloss = c.take<float>(n);
+  L.bsum = c.take<float>(n);
+  L.bcnt = c.take<int>(n);
+  L.bytes = align_up(c.off, 256);
+  return L;
+}
+
+int check_logits_args(long N, long V, int dtype, long ld, int reduction, float eps, int smooth) {
+  if (N < 0 || N > kMaxRows) return fail(CCE_ERR_INVALID_ARG, "N must be in [0, %ld] (got %ld)", kMaxRows, N);
+  if (V <= 0 || V > (1L << 30)) return fail(CCE_ERR_INVALID_ARG, "vocab size V must be in [1, 2^30] (got %ld)", V);
+  if (!logits_elem_size(dtype))
+    return fail(CCE_ERR_INVALID_ARG, "logits dtype must be CCE_DTYPE_BF16, CCE_DTYPE_F16 or CCE_DTYPE_F32");
+  if (ld < V) return fail(CCE_ERR_INVALID_ARG, "row stride %ld is smaller than V = %ld", ld, V);
+  if (reduction < CCE_REDUCTION_NONE || reduction > CCE_REDUCTION_SUM)
+    return fail(CCE_ERR_INVALID_ARG, "reduction must be 0 (none), 1 (mean) or 2 (sum), got %d", reduction);
+  if (!(eps >= 0.f && eps <= 1.f)) return fail(CCE_ERR_INVALID_ARG, "label_smoothing must be in [0, 1]");
+  if (smooth != CCE_SMOOTH_LOGV && smooth != CCE_SMOOTH_UNIFORM)
+    return fail(CCE_ERR_INVALID_ARG, "smoothing_form must be CCE_SMOOTH_LOGV or CCE_SMOOTH_UNIFORM, got %d", smooth);
+  return CCE_OK;
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -1881,6 +2134,105 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       if (rc) return rc;
     }
   }
+  return CCE_OK;
+}
+
+int cce_logits_forward_workspace_bytes(int64_t N, int64_t V, int reduction, size_t* bytes) {
+  g_err[0] = 0;
+  if (!bytes) return fail(CCE_ERR_INVALID_ARG, "bytes must not be null");
+  const int rc = check_logits_args(N, V, CCE_DTYPE_F32, V, reduction, 0.f, CCE_SMOOTH_LOGV);
+  if (rc) return rc;
+  *bytes = logits_layout(nullptr, N).bytes;
+  return CCE_OK;
+}
+
+int cce_logits_forward(const void* logits, int logits_dtype, int64_t ld, const void* labels, int labels_int64,
+                       int64_t N, int64_t V, int64_t ignore_index, float label_smoothing, float z_loss_weight,
+                       int smoothing_form, int reduction, float* loss_out, float* lse_out, int32_t* n_valid_out,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = check_logits_args(N, V, logits_dtype, ld, reduction, label_smoothing, smoothing_form);
+  if (rc) return rc;
+  // loss_out is [N] for 'none', so it may be null when N == 0
+  if (!n_valid_out || (!loss_out && (N > 0 || reduction != CCE_REDUCTION_NONE)) ||
+      (N > 0 && (!logits || !labels || !lse_out)))
+    return fail(CCE_ERR_INVALID_ARG, "logits, labels, loss_out, lse_out and n_valid_out must not be null");
+  const LogitsLayout need = logits_layout(nullptr, N);
+  if (workspace_bytes < need.bytes || !workspace)
+    return fail(CCE_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need.bytes, workspace_bytes);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const LogitsLayout L = logits_layout(workspace, N);
+  float* rowloss = reduction == CCE_REDUCTION_NONE ? loss_out : L.rowloss;
+  const float logV = logf((float)V);
+  if (N > 0) {
+    hipEvent_t e0, e1;
+    const bool timed = timing_begin(st, &e0, &e1);
+#define CCE_LAUNCH_LFWD(T)                                                                                        \
+  hipLaunchKernelGGL(ce_logits_fwd_kernel<T>, dim3((unsigned)N), dim3(256), 0, st, static_cast<const T*>(logits), \
+                     (long)ld, labels, labels_int64, (int)V, (long)ignore_index, label_smoothing, z_loss_weight,   \
+                     logV, smoothing_form, lse_out, rowloss, L.bsum, L.bcnt)
+    if (logits_dtype == CCE_DTYPE_BF16)
+      CCE_LAUNCH_LFWD(uint16_t);
+    else if (logits_dtype == CCE_DTYPE_F16)
+      CCE_LAUNCH_LFWD(_Float16);
+    else
+      CCE_LAUNCH_LFWD(float);
+#undef CCE_LAUNCH_LFWD
+    const hipError_t le = hipGetLastError();
+    if (timed) {
+      const double bytes = (double)N * (double)V * (double)logits_elem_size(logits_dtype);
+      timing_end(CCE_KERNEL_LOGITS_FWD, st, e0, e1, bytes, bytes);
+    }
+    HIP_TRY(le);
+  }
+  hipLaunchKernelGGL(fwd_finalize_kernel, dim3(1), dim3(1024), 0, st, L.bsum, L.bcnt, (int)N, reduction, loss_out,
+                     n_valid_out);
+  HIP_TRY(hipGetLastError());
+  return CCE_OK;
+}
+
+int cce_logits_backward(const float* grad_out, const void* logits, int logits_dtype, int64_t ld, const void* labels,
+                        int labels_int64, const float* lse, const int32_t* n_valid, int64_t N, int64_t V,
+                        int64_t ignore_index, float label_smoothing, float z_loss_weight, int smoothing_form,
+                        int reduction, void* grad_logits, int grad_dtype, int64_t ld_grad, void* stream) {
+  g_err[0] = 0;
+  int rc = check_logits_args(N, V, logits_dtype, ld, reduction, label_smoothing, smoothing_form);
+  if (rc) return rc;
+  if (grad_dtype != logits_dtype && grad_dtype != CCE_DTYPE_F32)
+    return fail(CCE_ERR_INVALID_ARG, "grad_dtype must be the logits' dtype or CCE_DTYPE_F32, got %d", grad_dtype);
+  if (ld_grad < V) return fail(CCE_ERR_INVALID_ARG, "gradient row stride %ld is smaller than V = %ld", (long)ld_grad, (long)V);
+  if (N == 0) return CCE_OK;
+  if (!grad_out || !logits || !labels || !lse || !n_valid || !grad_logits)
+    return fail(CCE_ERR_INVALID_ARG, "grad_out, logits, labels, lse, n_valid and grad_logits must not be null");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipEvent_t e0, e1;
+  const bool timed = timing_begin(st, &e0, &e1);
+#define CCE_LAUNCH_LBWD(T, TO)                                                                                       \
+  hipLaunchKernelGGL((ce_logits_bwd_kernel<T, TO>), dim3((unsigned)N), dim3(256), 0, st, grad_out,                   \
+                     static_cast<const T*>(logits), (long)ld, labels, labels_int64, lse, n_valid, (int)V,             \
+                     (long)ignore_index, label_smoothing, z_loss_weight, smoothing_form, reduction,                 \
+                     static_cast<TO*>(grad_logits), (long)ld_grad)
+  const bool f32_out = grad_dtype == CCE_DTYPE_F32;
+  if (logits_dtype == CCE_DTYPE_BF16) {
+    if (f32_out)
+      CCE_LAUNCH_LBWD(uint16_t, float);
+    else
+      CCE_LAUNCH_LBWD(uint16_t, uint16_t);
+  } else if (logits_dtype == CCE_DTYPE_F16) {
+    if (f32_out)
+      CCE_LAUNCH_LBWD(_Float16, float);
+    else
+      CCE_LAUNCH_LBWD(_Float16, _Float16);
+  } else {
+    CCE_LAUNCH_LBWD(float, float);
+  }
+#undef CCE_LAUNCH_LBWD
+  const hipError_t le = hipGetLastError();
+  if (timed) {
+    const double bytes = (double)N * (double)V * (double)(logits_elem_size(logits_dtype) + logits_elem_size(grad_dtype));
+    timing_end(CCE_KERNEL_LOGITS_BWD, st, e0, e1, bytes, bytes);
+  }
+  HIP_TRY(le);
   return CCE_OK;
 }
 

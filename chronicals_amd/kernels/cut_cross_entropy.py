@@ -28,6 +28,7 @@ import torch.nn as nn
 
 from .. import _lib
 from .. import ops as _ops  # noqa: F401  (registers chronicals_hip::cce_fwd / cce_bwd)
+from .logits_cross_entropy import ChunkedCrossEntropyLoss, chunked_cross_entropy_loss  # noqa: F401
 
 # Constants of the reference module (cut_cross_entropy.py:45-56), kept for
 # import compatibility.  The chunk size is the vocabulary band width of the
@@ -41,6 +42,8 @@ TRITON_BLOCK_SIZE_MAX = 65536 // 2
 
 __all__ = [
     "cut_cross_entropy",
+    "chunked_cross_entropy_loss",
+    "ChunkedCrossEntropyLoss",
     "CutCrossEntropyLoss",
     "CutCrossEntropyFunction",
     "get_optimal_chunk_size",

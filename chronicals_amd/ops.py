@@ -34,7 +34,7 @@ from torch import Tensor
 
 from . import _lib
 
-__all__ = ["cce_fwd", "cce_bwd"]
+__all__ = ["cce_fwd", "cce_bwd", "ce_logits_fwd", "ce_logits_bwd", "ce_logits_bwd_"]
 
 
 def _stream(device: torch.device) -> int:
@@ -138,3 +138,115 @@ def _cce_bwd_fake(grad_out, hidden, weight, labels, lse, n_valid, bias, ignore_i
     dw = hidden.new_empty((V, d) if need_dw else (0,), dtype=torch.float32 if dw_f32 else torch.bfloat16)
     db = hidden.new_empty((V,) if need_db else (0,), dtype=torch.float32)
     return dh, dw, db
+
+
+# ---------------------------------------------------------------------------
+# Cross-entropy over existing logits (cce_logits_forward / cce_logits_backward)
+#
+#   chronicals_hip::ce_logits_fwd(logits, labels, ignore_index, label_smoothing,
+#                                 z_loss_weight, smoothing_form, reduction)
+#                                 -> (loss, lse, n_valid)
+#   chronicals_hip::ce_logits_bwd(grad_out, logits, labels, lse, n_valid,
+#                                 ignore_index, label_smoothing, z_loss_weight,
+#                                 smoothing_form, reduction, f32_grad) -> grad_logits
+#   chronicals_hip::ce_logits_bwd_(... same ...)  overwrites logits with the gradient
+#
+# logits [N, V] bf16 / fp16 / fp32 with a contiguous last dimension (any row
+# stride).  ce_logits_bwd returns a contiguous [N, V] tensor of the logits'
+# dtype (fp32 when f32_grad).
+# ---------------------------------------------------------------------------
+
+_LOGITS_DTYPES = {torch.bfloat16: _lib.CCE_DTYPE_BF16, torch.float16: _lib.CCE_DTYPE_F16,
+                  torch.float32: _lib.CCE_DTYPE_F32}
+
+
+def _check_logits(logits: Tensor, labels: Tensor) -> None:
+    if logits.dtype not in _LOGITS_DTYPES:
+        raise RuntimeError(f"logits dtype {logits.dtype} not supported (bf16, fp16, fp32)")
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise RuntimeError(f"ce_logits ops take [N, V] logits with a contiguous last dimension, got "
+                           f"shape {tuple(logits.shape)} strides {logits.stride()}")
+    if labels.dim() != 1 or labels.shape[0] != logits.shape[0] or labels.dtype not in (torch.int64, torch.int32):
+        raise RuntimeError(f"ce_logits ops take int64/int32 labels [N], got {labels.dtype} {tuple(labels.shape)}")
+    if not labels.is_contiguous():
+        raise RuntimeError("labels must be contiguous")
+
+
+def _row_stride(t: Tensor) -> int:
+    return t.stride(0) if t.shape[0] > 1 else t.shape[1]
+
+
+@torch.library.custom_op("chronicals_hip::ce_logits_fwd", mutates_args=(), device_types="cuda")
+def ce_logits_fwd(logits: Tensor, labels: Tensor, ignore_index: int, label_smoothing: float, z_loss_weight: float,
+                  smoothing_form: int, reduction: int) -> Tuple[Tensor, Tensor, Tensor]:
+    _check_logits(logits, labels)
+    lib = _lib.load()
+    device = logits.device
+    N, V = logits.shape
+    with torch.cuda.device(device):
+        ws = torch.empty(_lib.logits_forward_workspace_bytes(N, V, reduction), dtype=torch.uint8, device=device)
+        loss = torch.empty((N,) if reduction == _lib.CCE_REDUCTION_NONE else (1,), dtype=torch.float32,
+                           device=device)
+        lse = torch.empty((N,), dtype=torch.float32, device=device)
+        n_valid = torch.empty((1,), dtype=torch.int32, device=device)
+        _lib.check(lib.cce_logits_forward(
+            logits.data_ptr(), _LOGITS_DTYPES[logits.dtype], _row_stride(logits), labels.data_ptr(),
+            int(labels.dtype == torch.int64), N, V, int(ignore_index), float(label_smoothing), float(z_loss_weight),
+            int(smoothing_form), int(reduction), loss.data_ptr(), lse.data_ptr(), n_valid.data_ptr(), ws.data_ptr(),
+            ws.numel(), _stream(device)))
+    return loss, lse, n_valid
+
+
+@ce_logits_fwd.register_fake
+def _ce_logits_fwd_fake(logits, labels, ignore_index, label_smoothing, z_loss_weight, smoothing_form, reduction):
+    N = logits.shape[0]
+    loss = logits.new_empty((N,) if reduction == _lib.CCE_REDUCTION_NONE else (1,), dtype=torch.float32)
+    return loss, logits.new_empty((N,), dtype=torch.float32), logits.new_empty((1,), dtype=torch.int32)
+
+
+def _logits_backward(grad_out: Tensor, logits: Tensor, labels: Tensor, lse: Tensor, n_valid: Tensor,
+                     ignore_index: int, label_smoothing: float, z_loss_weight: float, smoothing_form: int,
+                     reduction: int, out: Tensor) -> None:
+    _check_logits(logits, labels)
+    N, V = logits.shape
+    if N == 0:
+        return
+    lib = _lib.load()
+    device = logits.device
+    g = grad_out.detach().to(torch.float32).reshape(-1).contiguous()
+    with torch.cuda.device(device):
+        _lib.check(lib.cce_logits_backward(
+            g.data_ptr(), logits.data_ptr(), _LOGITS_DTYPES[logits.dtype], _row_stride(logits), labels.data_ptr(),
+            int(labels.dtype == torch.int64), lse.data_ptr(), n_valid.data_ptr(), N, V, int(ignore_index),
+            float(label_smoothing), float(z_loss_weight), int(smoothing_form), int(reduction), out.data_ptr(),
+            _LOGITS_DTYPES[out.dtype], _row_stride(out), _stream(device)))
+
+
+@torch.library.custom_op("chronicals_hip::ce_logits_bwd", mutates_args=(), device_types="cuda")
+def ce_logits_bwd(grad_out: Tensor, logits: Tensor, labels: Tensor, lse: Tensor, n_valid: Tensor, ignore_index: int,
+                  label_smoothing: float, z_loss_weight: float, smoothing_form: int, reduction: int,
+                  f32_grad: bool) -> Tensor:
+    dx = torch.empty(tuple(logits.shape), dtype=torch.float32 if f32_grad else logits.dtype, device=logits.device)
+    _logits_backward(grad_out, logits, labels, lse, n_valid, ignore_index, label_smoothing, z_loss_weight,
+                     smoothing_form, reduction, dx)
+    return dx
+
+
+@ce_logits_bwd.register_fake
+def _ce_logits_bwd_fake(grad_out, logits, labels, lse, n_valid, ignore_index, label_smoothing, z_loss_weight,
+                        smoothing_form, reduction, f32_grad):
+    return logits.new_empty(tuple(logits.shape), dtype=torch.float32 if f32_grad else logits.dtype)
+
+
+@torch.library.custom_op("chronicals_hip::ce_logits_bwd_", mutates_args=("logits",), device_types="cuda")
+def ce_logits_bwd_(grad_out: Tensor, logits: Tensor, labels: Tensor, lse: Tensor, n_valid: Tensor,
+                   ignore_index: int, label_smoothing: float, z_loss_weight: float, smoothing_form: int,
+                   reduction: int) -> None:
+    _logits_backward(grad_out, logits, labels, lse, n_valid, ignore_index, label_smoothing, z_loss_weight,
+                     smoothing_form, reduction, logits)
+
+
+@ce_logits_bwd_.register_fake
+def _ce_logits_bwd__fake(grad_out, logits, labels, lse, n_valid, ignore_index, label_smoothing, z_loss_weight,
+                         smoothing_form, reduction):
+    return None

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define CCE_ABI_VERSION 2
+#define CCE_ABI_VERSION 3
 
 #define CCE_OK 0
 #define CCE_ERR_INVALID_ARG 1
@@ -51,9 +51,15 @@ extern "C" {
 #define CCE_REDUCTION_MEAN 1
 #define CCE_REDUCTION_SUM 2
 
-/* gradient output element types */
+/* element types (gradient outputs; logits of the logits-in entry points) */
 #define CCE_DTYPE_BF16 0
 #define CCE_DTYPE_F32 1
+#define CCE_DTYPE_F16 2
+
+/* label-smoothing forms of the logits-in entry points */
+#define CCE_SMOOTH_LOGV 0    /* eps*log(V) (cut_cross_entropy.py:1237-1239)                   */
+#define CCE_SMOOTH_UNIFORM 1 /* eps*(lse - mean_v x), the uniform-target CE
+                                (triton_kernels.py:189-193, :2915, :2952-2956)               */
 
 /* Library ABI version (CCE_ABI_VERSION).  No reference counterpart. */
 int cce_abi_version(void);
@@ -109,15 +115,59 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
                  void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Cross-entropy over logits that already exist (no lm_head fusion): the
+ * callers that hold logits.  Replaces the row computation of
+ *   chunked_cross_entropy_loss  cut_cross_entropy.py:1169-1249  (CCE_SMOOTH_LOGV)
+ *   _liger_ce_kernel            triton_kernels.py:2839-2963     (CCE_SMOOTH_UNIFORM)
+ *   fused_cross_entropy_kernel  triton_kernels.py:141-210       (CCE_SMOOTH_UNIFORM)
+ * For logits [N][ld] (row stride ld >= V elements, last dimension
+ * contiguous; bf16, fp16 or fp32 per logits_dtype):
+ *   lse[n] = log(sum_v exp(x[n][v]) + 1e-10)                   (:1206-1223)
+ *   row[n] = valid ? (1-eps)*(lse - x[n][label]) + eps*S + z*lse^2 : 0
+ *            S = log(V) (CCE_SMOOTH_LOGV, :1226-1246) or
+ *            S = lse - sum_v x[n][v]/V (CCE_SMOOTH_UNIFORM, triton_kernels.py:2952-2956)
+ *   loss   = mean: sum(row)/max(n_valid,1); sum: sum(row); none: row[N]
+ * A label outside [0, V) that is not ignore_index has no target logit (the
+ * chunked reference's gather would raise; the Triton kernels give the same
+ * zero target).  Deterministic; workspace from
+ * cce_logits_forward_workspace_bytes.
+ */
+int cce_logits_forward_workspace_bytes(int64_t N, int64_t V, int reduction, size_t* bytes);
+int cce_logits_forward(const void* logits, int logits_dtype, int64_t ld, const void* labels, int labels_int64,
+                       int64_t N, int64_t V, int64_t ignore_index, float label_smoothing, float z_loss_weight,
+                       int smoothing_form, int reduction, float* loss_out, float* lse_out, int32_t* n_valid_out,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Gradient of cce_logits_forward's loss with respect to the logits, for
+ * valid rows (zero rows for ignored labels), p = softmax(x[n]):
+ *   CCE_SMOOTH_LOGV:    g_n*(((1-eps) + 2z*lse[n])*p[v] - (1-eps)*[v == label])
+ *                       (autograd through cut_cross_entropy.py:1169-1249;
+ *                       eps*log V is a constant)
+ *   CCE_SMOOTH_UNIFORM: g_n*((1 + 2z*lse[n])*p[v] - eps/V - (1-eps)*[v == label])
+ *                       (triton_kernels.py:2930-2947, :197-206)
+ * g_n as in cce_backward.  grad_logits has row stride ld_grad and element type
+ * grad_dtype: the logits' type or CCE_DTYPE_F32.  grad_logits may be the
+ * logits buffer itself (same type and stride): the gradient then overwrites
+ * the logits, as _liger_ce_kernel does.
+ */
+int cce_logits_backward(const float* grad_out, const void* logits, int logits_dtype, int64_t ld, const void* labels,
+                        int labels_int64, const float* lse, const int32_t* n_valid, int64_t N, int64_t V,
+                        int64_t ignore_index, float label_smoothing, float z_loss_weight, int smoothing_form,
+                        int reduction, void* grad_logits, int grad_dtype, int64_t ld_grad, void* stream);
+
+/*
  * Per-kernel timing for measurement tools (no counterpart in the reference).
- * While enabled, every GEMM launch of cce_forward / cce_backward is bracketed
+ * While enabled, every GEMM launch of cce_forward / cce_backward and every
+ * row-kernel launch of cce_logits_forward / cce_logits_backward is bracketed
  * by HIP events recorded on its stream.  cce_kernel_timing_read() waits for
  * the recorded events and returns, for one kernel kind, the summed
- * milliseconds, the launch count and the MFMA FLOPs of those launches —
- * credited (the algorithmic work: forward logits, dHidden, dWeight; the
- * backward's logits recompute is executed but not credited) and executed —
- * then clears that kind's record.  credited_flops / executed_flops may be
- * NULL.  Kinds:
+ * milliseconds, the launch count and the work of those launches — credited
+ * (the algorithmic work: forward logits, dHidden, dWeight; the backward's
+ * logits recompute is executed but not credited) and executed — then clears
+ * that kind's record.  The work is MFMA FLOPs for the GEMM kinds and
+ * algorithmic HBM bytes for the two logits kinds.  credited_flops /
+ * executed_flops may be NULL.  Kinds:
  */
 #define CCE_KERNEL_FWD_LSE 0   /* forward GEMM + online logsumexp                 */
 #define CCE_KERNEL_BWD_GRAD 1  /* backward recompute GEMM -> dLoss/dS             */
@@ -126,7 +176,9 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
 #define CCE_KERNEL_BWD_DHDW 4  /* dHidden + dWeight GEMMs in one launch            */
 #define CCE_KERNEL_BWD_BAND 5  /* dHidden + dWeight of band b with the recompute
                                   of band b+1 in one launch                        */
-#define CCE_KERNEL_KINDS 6
+#define CCE_KERNEL_LOGITS_FWD 6 /* logits-in forward row kernel (reads N*V)     */
+#define CCE_KERNEL_LOGITS_BWD 7 /* logits-in backward row kernel (N*V in + out) */
+#define CCE_KERNEL_KINDS 8
 int cce_kernel_timing_enable(int enable);
 int cce_kernel_timing_read(int kind, double* total_ms, int64_t* launches, double* credited_flops,
                            double* executed_flops);

@@ -22,6 +22,25 @@ A numpy restatement of the reference's PyTorch CPU algorithm
               :792); dH += G W_c (:795), dW_c = G^T H (:798), dB_c = sum G
               (:801-802).
 
+  logits_forward()   cross-entropy over existing logits [N, V]:
+              smoothing='logv' follows chunked_cross_entropy_loss,
+              cut_cross_entropy.py:1199-1249: per V-chunk online max and
+              rescaled sum-exp (:1210-1221), lse = m + log(s + 1e-10) (:1223),
+              target gather with ignored rows zeroed (:1226-1231),
+              (1-eps)*ce + eps*log(V) (:1234-1239), z*lse^2 (:1242-1243),
+              mask and sum / max(n_valid, 1) (:1246-1249).
+              smoothing='uniform' follows _liger_ce_kernel,
+              triton_kernels.py:2886-2963: the same online pass per block
+              (:2893-2911) plus smooth_sum = -eps/V * sum(x) (:2914-2915),
+              loss = (1-eps)*(lse - t) + smooth_sum + eps*lse (:2952-2956),
+              + z*lse^2 (:2959); which is also fused_cross_entropy_kernel's
+              loss (:175-194).
+  logits_backward()  dLoss/dlogits of logits_forward(): 'logv' is what
+              autograd gives through :1199-1249, (1-eps)*(p - onehot)
+              + 2z*lse*p; 'uniform' is :2930-2947 (and :197-206),
+              p - eps/V - (1-eps)*onehot + 2z*lse*p; times g_n
+              (grad_out, divided by max(n_valid, 1) for 'mean', :2946-2947).
+
 The reference's CPU backward loses the one-hot term: its scatter_add_ at
 :776-780 writes into a boolean-mask copy.  backward() applies the term by
 default (as the reference's GPU path, :530-546, and its sibling
@@ -29,7 +48,8 @@ FusedLinearCrossEntropyFunction, triton_kernels.py:2594-2601, do);
 ``apply_onehot=False`` reproduces the as-shipped CPU gradient and exists only
 so tests can show the pinning checks reject it.
 
-Parity pins (tests/test_oracle.py): every function here is checked against
+Parity pins (tests/test_oracle.py, tests/test_oracle_logits.py): every
+function here is checked against
 an independent float64 closed form (torch's logsumexp / cross_entropy with
 autograd, including torch's own label_smoothing, and brute-force Python sums
 on tiny inputs), special cases (W = 0 gives loss log V; all rows ignored
@@ -165,3 +185,89 @@ def loss_and_grads(hidden, weight, labels, bias=None, chunk_size=8192, ignore_in
     gh, gw, gb = backward(hidden, weight, labels, lse, valid, grad_output, bias, chunk_size, ignore_index,
                           label_smoothing, z_loss_weight, reduction, True, dtype)
     return loss, lse, gh, gw, gb
+
+
+SMOOTHING_FORMS = ("logv", "uniform")
+
+
+def logits_forward(logits: np.ndarray, labels: np.ndarray, chunk_size: int = 8192, ignore_index: int = -100,
+                   label_smoothing: float = 0.0, z_loss_weight: float = 0.0, reduction: str = "mean",
+                   smoothing: str = "logv", dtype=np.float32):
+    """Cross-entropy over logits [..., V].  Returns (loss, lse [N], valid_mask [N])."""
+    if reduction not in REDUCTIONS:
+        raise ValueError(reduction)
+    if smoothing not in SMOOTHING_FORMS:
+        raise ValueError(smoothing)
+    x = np.asarray(logits)
+    V = x.shape[-1]
+    x = x.reshape(-1, V).astype(dtype, copy=False)
+    lab = np.asarray(labels).reshape(-1)
+    n = x.shape[0]
+    max_logit = np.full(n, -np.inf, dtype=dtype)
+    sum_exp = np.zeros(n, dtype=dtype)
+    smooth_sum = np.zeros(n, dtype=dtype)
+    for c0 in range(0, V, chunk_size):
+        xc = x[:, c0:min(c0 + chunk_size, V)]
+        cmax = xc.max(axis=1) if n else np.zeros(0, dtype)
+        new_max = np.maximum(max_logit, cmax)
+        sum_exp = sum_exp * np.exp(max_logit - new_max)
+        max_logit = new_max
+        sum_exp = sum_exp + np.exp(xc - max_logit[:, None]).sum(axis=1, dtype=dtype)
+        if smoothing == "uniform":
+            smooth_sum = smooth_sum + (dtype(-label_smoothing / V) * xc).sum(axis=1, dtype=dtype)
+    lse = (max_logit + np.log(sum_exp + dtype(1e-10))).astype(dtype)
+    valid = lab != ignore_index
+    has_t = valid & (lab >= 0) & (lab < V)
+    target = np.zeros(n, dtype=dtype)
+    rows = np.nonzero(has_t)[0]
+    target[rows] = x[rows, lab[rows]]
+    ce = lse - target
+    if smoothing == "logv":
+        if label_smoothing > 0.0:
+            ce = (1.0 - label_smoothing) * ce + label_smoothing * math.log(V)
+    elif label_smoothing > 0.0:
+        ce = ce * (1.0 - label_smoothing) + (smooth_sum + label_smoothing * lse)
+    total = (ce + z_loss_weight * lse ** 2).astype(dtype) * valid.astype(dtype)
+    n_valid = max(int(valid.sum()), 1)
+    if reduction == "mean":
+        loss = dtype(total.sum(dtype=np.float64) / n_valid)
+    elif reduction == "sum":
+        loss = dtype(total.sum(dtype=np.float64))
+    else:
+        loss = total
+    return loss, lse, valid
+
+
+def logits_backward(logits: np.ndarray, labels: np.ndarray, lse: np.ndarray, valid_mask: np.ndarray, grad_output,
+                    label_smoothing: float = 0.0, z_loss_weight: float = 0.0, reduction: str = "mean",
+                    smoothing: str = "logv", dtype=np.float32) -> np.ndarray:
+    """dLoss/dlogits [N, V] of logits_forward() times grad_output."""
+    if smoothing not in SMOOTHING_FORMS:
+        raise ValueError(smoothing)
+    x = np.asarray(logits)
+    V = x.shape[-1]
+    x = x.reshape(-1, V).astype(dtype, copy=False)
+    lab = np.asarray(labels).reshape(-1)
+    n = x.shape[0]
+    valid = np.asarray(valid_mask).reshape(-1)
+    lse = np.asarray(lse, dtype=dtype).reshape(-1)
+    go = np.asarray(grad_output, dtype=np.float64).reshape(-1)
+    n_valid = max(int(valid.sum()), 1)
+    if reduction == "mean":
+        scale = np.full(n, go[0] / n_valid)
+    elif reduction == "sum":
+        scale = np.full(n, go[0])
+    else:
+        scale = go.copy()
+    scale = (scale * valid).astype(dtype)
+    p = np.exp(x - lse[:, None])
+    eps = label_smoothing
+    if smoothing == "logv":
+        g = dtype(1.0 - eps) * p
+    else:
+        g = p - dtype(eps / V)
+    if z_loss_weight > 0.0:
+        g = g + dtype(2.0 * z_loss_weight) * lse[:, None] * p
+    rows = np.nonzero(valid & (lab >= 0) & (lab < V))[0]
+    g[rows, lab[rows]] -= dtype(1.0 - eps)
+    return (g * scale[:, None]).astype(dtype)
