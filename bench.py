@@ -12,6 +12,12 @@ recompute, which is executed but not credited, as the algorithmic work of a
 fwd+bwd step is 6*N*V*d FLOPs) is timed with HIP events on its own launch
 stream by the library (cce_kernel_timing_enable) over the timed region; the
 library reports each launch's credited and executed FLOPs.
+
+``--workload logits`` measures the logits-in cross-entropy instead
+(chunked_cross_entropy_loss over [N, V] bf16 logits of the same C2 shape,
+forward + backward producing dlogits); its kernels are HBM-bound and the
+roofline is algorithmic bytes (N*V*2 read forward; N*V*2 read + N*V*2
+written backward) over the HIP-event launch time.
 """
 from __future__ import annotations
 
@@ -30,6 +36,7 @@ if REPO not in sys.path:
 PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 4096 FLOP/clk x 2.4 GHz (dense bf16 MFMA)
 PEAK_HBM_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
+TRAFFIC_LOGITS_FILE = os.path.join(REPO, "profiles", "traffic_logits.json")
 
 
 def cpu_model() -> str:
@@ -68,6 +75,37 @@ def cpu_baseline(cfg, rows: int, seed: int = 0) -> dict:
             "cpu": cpu_model()}
 
 
+def cpu_baseline_logits(cfg, rows: int, seed: int = 0) -> dict:
+    """Oracle (numpy restatement of chunked_cross_entropy_loss + its gradient) on a row slice; tokens/s."""
+    import numpy as np
+    import torch
+
+    from oracle import cce_oracle
+
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(rows, cfg.V, generator=g) * 3.0).to(torch.bfloat16).float().numpy()
+    lab = torch.randint(0, cfg.V, (rows,), generator=g).numpy()
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+    def run(xs, ls):
+        loss, lse, valid = cce_oracle.logits_forward(xs, ls, 8192)
+        return cce_oracle.logits_backward(xs, ls, lse, valid, np.ones(1))
+
+    run(x[: max(8, rows // 8)], lab[: max(8, rows // 8)])
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run(x, lab)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": rows / t, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{rows} rows of [N={cfg.N}, V={cfg.V}] logits (bf16 values in fp32); numpy restatement of "
+                      f"chunked_cross_entropy_loss forward (V-chunk 8192) + its gradient, single-threaded "
+                      f"elementwise numpy; median of 3 runs after a warm-up, {t:.2f} s per run; tokens/s = rows / "
+                      f"time (linear in N)",
+            "cpu": cpu_model()}
+
+
 def copy_calibration(nbytes: int) -> None:
     """A plain device copy of known size, for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters."""
     import torch
@@ -88,10 +126,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="C2")
     ap.add_argument("--chunk", type=int, default=8192)
-    ap.add_argument("--cpu-rows", type=int, default=4096)
+    ap.add_argument("--cpu-rows", type=int, default=None,
+                    help="rows of the CPU baseline sample (default 4096 fused, 8192 logits)")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (PMC calibration) and exit")
+    ap.add_argument("--workload", choices=("fused", "logits"), default="fused",
+                    help="fused: linear-CE from hidden + lm_head (default); logits: CE over existing logits")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -101,6 +142,9 @@ def main() -> int:
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return 0
+
+    if args.workload == "logits":
+        return bench_logits(args)
 
     import torch
 
@@ -214,7 +258,103 @@ def main() -> int:
         "loss": float(loss.item()),
     }
     if not args.skip_cpu:
-        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_rows)
+        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_rows or 4096)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def bench_logits(args) -> int:
+    """chunked_cross_entropy_loss fwd+bwd over [N, V] bf16 logits of config C2's shape."""
+    import torch
+
+    from chronicals_amd import _lib
+    from chronicals_amd.kernels.logits_cross_entropy import chunked_cross_entropy_loss
+    from tests.cce_common import CONFIGS
+
+    cfg = CONFIGS[args.config]
+    N, V = cfg.N, cfg.V
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = (torch.randn(N, V, generator=g, device=dev) * 3.0).to(torch.bfloat16).requires_grad_(True)
+    lab = torch.randint(0, V, (N,), generator=g, device=dev)
+    lab[torch.rand(N, generator=g, device=dev) < cfg.ignore_frac] = -100
+
+    def step():
+        x.grad = None
+        loss = chunked_cross_entropy_loss(x, lab)
+        loss.backward()
+        return loss
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    for k in range(_lib.CCE_KERNEL_KINDS):
+        _lib.kernel_timing_read(k)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    _lib.kernel_timing_enable(True)
+    torch.cuda.synchronize()
+    evs[0].record()
+    for i in range(args.steps):
+        loss = step()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    _lib.kernel_timing_enable(False)
+    ms = evs[0].elapsed_time(evs[-1]) / args.steps
+    step_ms = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps))
+
+    def pct(q):
+        return step_ms[min(len(step_ms) - 1, int(round(q * (len(step_ms) - 1))))]
+
+    kernels = {}
+    for k in (_lib.CCE_KERNEL_LOGITS_FWD, _lib.CCE_KERNEL_LOGITS_BWD):
+        tot_ms, n, by, _ = _lib.kernel_timing_read(k)
+        if n == 0:
+            continue
+        kernels[_lib.KERNEL_KIND_NAMES[k]] = {
+            "launches_per_step": n / args.steps,
+            "avg_launch_us": tot_ms / n * 1e3,
+            "ms_per_step": tot_ms / args.steps,
+            "algorithmic_gb_per_launch": by / n / 1e9,
+            "gbs": by / (tot_ms * 1e-3) / 1e9,
+        }
+    dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
+    kd = kernels[dom]
+    step_bytes = 3.0 * N * V * 2
+    traffic = None
+    try:
+        with open(TRAFFIC_LOGITS_FILE) as f:
+            tr = json.load(f)
+        if tr.get("config") == cfg.name and tr.get("kernel") == dom:
+            traffic = tr.get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        pass
+    out = {
+        "metric": "logits-in CE fwd+bwd tokens/s and % HBM peak, N=16k V=152k bf16 logits",
+        "value": N / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "step_ms": {"median": pct(0.5), "p10": pct(0.1), "p90": pct(0.9)},
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,9) bf16 logits, uniform labels, 5% ignore_index)",
+        "config": {"workload": f"logits-in CE (chunked_cross_entropy_loss) fwd+bwd over [{N}, {V}] bf16 logits, "
+                               f"mean; grad dlogits bf16", "N": N, "V": V},
+        "step_gbs_algorithmic": step_bytes / (ms * 1e-3) / 1e9,
+        "roofline": {"bound": "hbm", "achieved": kd["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": kd["gbs"] / PEAK_HBM_GBS, "traffic": traffic,
+                     "kernel": f"{dom}: algorithmic bytes per launch ({kd['algorithmic_gb_per_launch']:.2f} GB) "
+                               f"over its HIP-event average launch time ({kd['avg_launch_us']:.1f} us)"},
+        "kernels": kernels,
+        "loss": float(loss.item()),
+    }
+    if not args.skip_cpu:
+        out["cpu_baseline"] = cpu_baseline_logits(cfg, args.cpu_rows or 8192)
     print(json.dumps(out), flush=True)
     return 0
 
