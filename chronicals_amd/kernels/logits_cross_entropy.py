@@ -20,6 +20,11 @@ again and writes the gradient.
       reference triton_kernels.py:141-257 and :2206-2218.  Returns the mean
       loss and the per-row (unnormalised) gradient in fp32, as the reference
       kernel does.
+  compute_padding_free_loss, compute_packed_loss
+      reference chronicals/data/sequence_packer.py:1660-1717 and
+      sequence_packer_v2.py:1058-1113: the packed-sequence losses, torch's
+      label-smoothed cross-entropy (the uniform form) per token, weighted by an
+      optional ``loss_mask`` and divided by its sum ('mean').
 
 Deliberate differences from the reference:
   * Tensors must live on a HIP device; there is no CPU path.
@@ -34,6 +39,8 @@ Deliberate differences from the reference:
   * With every label ignored, ``liger_cross_entropy_forward`` returns a zero
     gradient (the reference returns the logits unchanged, :3026-3027, which is
     no gradient of the zero loss).
+  * Losses are fp32 whatever the logits' dtype (torch's cross_entropy, which
+    the packed-sequence losses call, returns the logits' dtype).
 """
 from __future__ import annotations
 
@@ -55,6 +62,8 @@ __all__ = [
     "fused_cross_entropy",
     "fused_cross_entropy_triton",
     "LogitsCrossEntropyFunction",
+    "compute_padding_free_loss",
+    "compute_packed_loss",
 ]
 
 TRITON_BLOCK_SIZE_MAX = 65536 // 2  # reference triton_kernels.py:2835, kept for import compatibility
@@ -281,3 +290,58 @@ def fused_cross_entropy_triton(
 
 
 fused_cross_entropy = fused_cross_entropy_triton  # reference :2206-2218 dispatches here on a GPU
+
+
+# ---------------------------------------------------------------------------
+# sequence_packer.py:1660-1717, sequence_packer_v2.py:1058-1113
+# ---------------------------------------------------------------------------
+
+def compute_padding_free_loss(
+    logits: torch.Tensor,
+    labels: torch.Tensor,
+    loss_mask=None,
+    ignore_index: int = -100,
+    reduction: str = "mean",
+    label_smoothing: float = 0.0,
+) -> torch.Tensor:
+    """Cross-entropy of packed sequences (reference sequence_packer.py:1660-1717).
+
+    Per token: torch's label-smoothed cross-entropy
+    (1-eps)*(lse - x[label]) + eps*(lse - mean(x)), 0 where the label is
+    ``ignore_index``.  Without ``loss_mask``: 'mean' divides the sum by the
+    number of labels that are not ``ignore_index`` (at least 1).  With it, each
+    token's loss is multiplied by its mask value and 'mean' divides by the
+    mask's sum (at least 1).  'none' returns the flat per-token losses.
+    """
+    red = _reduction_code(reduction)
+    x, lab = _rows(logits, labels, "compute_padding_free_loss")
+    if loss_mask is None:
+        return LogitsCrossEntropyFunction.apply(x, lab, ignore_index, label_smoothing, 0.0,
+                                                _lib.CCE_SMOOTH_UNIFORM, red)
+    rows = LogitsCrossEntropyFunction.apply(x, lab, ignore_index, label_smoothing, 0.0, _lib.CCE_SMOOTH_UNIFORM,
+                                            _lib.CCE_REDUCTION_NONE)
+    m = loss_mask.reshape(-1).to(rows.dtype)
+    if m.numel() != rows.numel():
+        raise RuntimeError(f"loss_mask has {m.numel()} elements, expected {rows.numel()}")
+    rows = rows * m
+    if red == _lib.CCE_REDUCTION_MEAN:
+        return rows.sum() / m.sum().clamp(min=1.0)
+    if red == _lib.CCE_REDUCTION_SUM:
+        return rows.sum()
+    return rows
+
+
+def compute_packed_loss(
+    logits: torch.Tensor,
+    labels: torch.Tensor,
+    loss_mask=None,
+    ignore_index: int = -100,
+    reduction: str = "mean",
+    label_smoothing: float = 0.0,
+) -> torch.Tensor:
+    """Cross-entropy of packed sequences (reference sequence_packer_v2.py:1058-1113).
+
+    logits [total_tokens, V] or [batch, seq, V]; the same loss as
+    compute_padding_free_loss.
+    """
+    return compute_padding_free_loss(logits, labels, loss_mask, ignore_index, reduction, label_smoothing)

@@ -136,3 +136,65 @@ def test_custom_op_has_no_cpu_kernel():
     with pytest.raises(NotImplementedError):
         torch.ops.chronicals_hip.cce_fwd(torch.zeros(4, 8, dtype=torch.bfloat16), torch.zeros(5, 8, dtype=torch.bfloat16),
                                          torch.zeros(4, dtype=torch.int64), None, -100, 0.0, 0.0, 1)
+
+
+# ---------------------------------------------------------------------------
+# Logits-in cross-entropy (chronicals_amd/kernels/logits_cross_entropy.py)
+# ---------------------------------------------------------------------------
+
+def test_logits_api_signatures_match_reference():
+    from chronicals_amd.kernels import logits_cross_entropy as lce
+    sig = lambda f: list(inspect.signature(f).parameters)  # noqa: E731
+    # cut_cross_entropy.py:1169-1176 (+ reduction)
+    assert sig(lce.chunked_cross_entropy_loss)[:6] == ["logits", "labels", "chunk_size", "ignore_index",
+                                                       "label_smoothing", "z_loss_weight"]
+    # triton_kernels.py:2979-2987, :3109-3116, :213-219
+    assert sig(lce.liger_cross_entropy_forward) == ["logits", "target", "ignore_index", "lse_square_scale",
+                                                    "label_smoothing", "reduction", "compute_grads"]
+    assert sig(lce.liger_cross_entropy) == ["logits", "target", "ignore_index", "lse_square_scale",
+                                            "label_smoothing", "reduction"]
+    assert sig(lce.fused_cross_entropy) == ["logits", "labels", "label_smoothing", "z_loss_weight", "ignore_index"]
+    assert inspect.signature(lce.fused_cross_entropy).parameters["z_loss_weight"].default == 1e-4
+    # sequence_packer.py:1660-1667, sequence_packer_v2.py:1058-1065
+    for f in (lce.compute_padding_free_loss, lce.compute_packed_loss):
+        assert sig(f) == ["logits", "labels", "loss_mask", "ignore_index", "reduction", "label_smoothing"]
+    m = lce.ChunkedCrossEntropyLoss()
+    assert (m.chunk_size, m.ignore_index, m.label_smoothing, m.z_loss_weight) == (8192, -100, 0.0, 0.0)
+    assert cce.chunked_cross_entropy_loss is lce.chunked_cross_entropy_loss
+    assert cce.ChunkedCrossEntropyLoss is lce.ChunkedCrossEntropyLoss
+
+
+def test_logits_apis_refuse_cpu_tensors():
+    from chronicals_amd.kernels import logits_cross_entropy as lce
+    x = torch.randn(2, 3, 10)
+    lab = torch.zeros(2, 3, dtype=torch.long)
+    for call in (lambda: lce.chunked_cross_entropy_loss(x, lab),
+                 lambda: lce.liger_cross_entropy(x, lab),
+                 lambda: lce.liger_cross_entropy_forward(x, lab),
+                 lambda: lce.fused_cross_entropy(x, lab),
+                 lambda: lce.compute_padding_free_loss(x, lab),
+                 lambda: lce.compute_packed_loss(x, lab, torch.ones(2, 3))):
+        with pytest.raises(RuntimeError, match="HIP devices"):
+            call()
+
+
+def test_logits_ops_fake_shapes():
+    import chronicals_amd.ops  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        x = torch.empty(300, 1000, dtype=torch.float16, device="cuda")
+        lab = torch.empty(300, dtype=torch.int64, device="cuda")
+        for red, shape in ((0, (300,)), (1, (1,)), (2, (1,))):
+            loss, lse, nv = torch.ops.chronicals_hip.ce_logits_fwd(x, lab, -100, 0.1, 0.0, 1, red)
+            assert tuple(loss.shape) == shape and loss.dtype == torch.float32
+            assert tuple(lse.shape) == (300,) and tuple(nv.shape) == (1,) and nv.dtype == torch.int32
+        for f32, dt in ((False, torch.float16), (True, torch.float32)):
+            g = torch.ops.chronicals_hip.ce_logits_bwd(loss, x, lab, lse, nv, -100, 0.1, 0.0, 1, 1, f32)
+            assert tuple(g.shape) == (300, 1000) and g.dtype == dt
+
+
+def test_logits_ops_have_no_cpu_kernel():
+    import chronicals_amd.ops  # noqa: F401
+    with pytest.raises(NotImplementedError):
+        torch.ops.chronicals_hip.ce_logits_fwd(torch.zeros(4, 8), torch.zeros(4, dtype=torch.int64), -100, 0.0, 0.0,
+                                               0, 1)
