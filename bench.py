@@ -119,6 +119,39 @@ def copy_calibration(nbytes: int) -> None:
     print(json.dumps({"copy_calibration_bytes": nbytes, "launches": 3}), flush=True)
 
 
+def blas_reference(cfg, chunk: int) -> None:
+    """Library speed-of-light reference: torch.matmul (hipBLASLt) bf16 GEMMs of the path's shapes at cfg, each
+    timed with events over 10 calls after 3 warm-ups; one JSON line per GEMM."""
+    import torch
+
+    N, d, V = cfg.N, cfg.d, cfg.V
+
+    def run(name, M, Nn, K, a_t=False, b_t=True):
+        a = (torch.randn(K, M, device="cuda").to(torch.bfloat16).t() if a_t
+             else torch.randn(M, K, device="cuda").to(torch.bfloat16))
+        b = torch.randn(Nn, K, device="cuda").to(torch.bfloat16).t() if b_t else torch.randn(K, Nn, device="cuda").to(
+            torch.bfloat16)
+        for _ in range(3):
+            a @ b
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            a @ b
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 10
+        print(json.dumps({"blas_reference": name, "M": M, "N": Nn, "K": K, "us": ms * 1e3,
+                          "tflops": 2.0 * M * Nn * K / (ms * 1e-3) / 1e12}), flush=True)
+        del a, b
+
+    run("8192^3 A.B^T", 8192, 8192, 8192)
+    run(f"{cfg.name} forward logits H.W^T", N, V, d)
+    run(f"{cfg.name} band recompute H.W_b^T", N, chunk, d)
+    run(f"{cfg.name} band dH G_b.W_b", N, d, chunk, b_t=False)
+    run(f"{cfg.name} band dW G_b^T.H", chunk, d, N, a_t=True, b_t=False)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -131,6 +164,8 @@ def main() -> int:
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (PMC calibration) and exit")
+    ap.add_argument("--blas-reference", action="store_true",
+                    help="only time torch.matmul (hipBLASLt) on the path's GEMM shapes and exit")
     ap.add_argument("--workload", choices=("fused", "logits"), default="fused",
                     help="fused: linear-CE from hidden + lm_head (default); logits: CE over existing logits")
     args = ap.parse_args()
@@ -145,6 +180,10 @@ def main() -> int:
 
     if args.workload == "logits":
         return bench_logits(args)
+    if args.blas_reference:
+        from tests.cce_common import CONFIGS
+        blas_reference(CONFIGS[args.config], args.chunk)
+        return 0
 
     import torch
 
