@@ -1136,8 +1136,8 @@ __device__ inline long load_label(const void* labels, int is64, long n) {
 __global__ __launch_bounds__(256) void fwd_combine_kernel(
     const float* __restrict__ pm, const float* __restrict__ ps, int splits, const bf16_t* __restrict__ H,
     const bf16_t* __restrict__ W, const void* labels, int labels64, const float* __restrict__ bias, int N, int d,
-    int V, long ignore_index, float eps, float zw, float logV, float* __restrict__ lse_out,
-    float* __restrict__ rowloss, float* __restrict__ bsum, int* __restrict__ bcnt) {
+    int V, long ignore_index, float eps, float zw, float logV, const float* __restrict__ wsum,
+    float* __restrict__ lse_out, float* __restrict__ rowloss, float* __restrict__ bsum, int* __restrict__ bcnt) {
   const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int n = blockIdx.x * 4 + w;
   __shared__ float s_loss[4];
@@ -1180,9 +1180,27 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(
       for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o);
       t = dot + (bias ? bias[lab] : 0.f);
     }
+    // uniform-target smoothing: the row mean of the logits is H[n].(sum_v W[v]) / V
+    // (+ mean bias); wsum = {sum_v W[v][0..d), sum_v bias[v]}
+    float smooth = logV;
+    if (valid && eps > 0.f && wsum) {
+      const bf16_t* h = H + (long)n * d;
+      float dot = 0.f;
+      for (int k = l * 8; k < d; k += 512) {
+        const u32x4 hv = *reinterpret_cast<const u32x4*>(h + k);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          dot += bf16_to_f32(hv[q] & 0xffffu) * wsum[k + 2 * q];
+          dot += bf16_to_f32(hv[q] >> 16) * wsum[k + 2 * q + 1];
+        }
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o);
+      smooth = lse - (dot + wsum[d]) / (float)V;
+    }
     if (valid) {
       float ce = lse - t;
-      if (eps > 0.f) ce = (1.f - eps) * ce + eps * logV;
+      if (eps > 0.f) ce = (1.f - eps) * ce + eps * smooth;
       loss = ce + zw * lse * lse;
       cnt = 1;
     }
@@ -1514,15 +1532,18 @@ __global__ __launch_bounds__(256) void transpose_kernel(const bf16_t* __restrict
 // dB[c] = sum_m G[m][c] for c < C (fixed order: deterministic).  Block = 64 columns.
 __global__ __launch_bounds__(256) void colsum_kernel(const bf16_t* __restrict__ G, long ldg, int M, int C,
                                                      float* __restrict__ out) {
+  // blockIdx.y = row split: rows [y*M/gridDim.y, (y+1)*M/gridDim.y) into out[y][C]
   __shared__ float part[32][65];
   const int tid = threadIdx.x;
   const int cg = tid & 7, rg = tid >> 3;  // 8 column groups of 8, 32 row groups
   const int c0 = blockIdx.x * 64 + cg * 8;
+  const int m0 = (int)(((long)M * blockIdx.y) / gridDim.y), m1 = (int)(((long)M * (blockIdx.y + 1)) / gridDim.y);
+  out += (long)blockIdx.y * C;
   float a[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) a[e] = 0.f;
   if (c0 < C) {
-    for (int m = rg; m < M; m += 32) {
+    for (int m = m0 + rg; m < m1; m += 32) {
       const u32x4 v = *reinterpret_cast<const u32x4*>(G + (long)m * ldg + c0);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -1539,6 +1560,32 @@ __global__ __launch_bounds__(256) void colsum_kernel(const bf16_t* __restrict__ 
     for (int r = 0; r < 32; ++r) s += part[r][tid];
     const int c = blockIdx.x * 64 + tid;
     if (c < C) out[c] = s;
+  }
+}
+
+// out[c] = sum over r of part[r][c] in order r = 0..R-1; block 0 also writes
+// out[C] = sum of vec[0..n) (fixed-order tree), or 0 without vec.
+__global__ __launch_bounds__(256) void sum_parts_kernel(const float* __restrict__ part, int R, int C,
+                                                        const float* __restrict__ vec, int n,
+                                                        float* __restrict__ out) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c < C) {
+    float s = 0.f;
+    for (int r = 0; r < R; ++r) s += part[(long)r * C + c];
+    out[c] = s;
+  }
+  if (blockIdx.x == 0) {
+    __shared__ float red[256];
+    float a = 0.f;
+    if (vec)
+      for (int i = threadIdx.x; i < n; i += 256) a += vec[i];
+    red[threadIdx.x] = a;
+    __syncthreads();
+    for (int o = 128; o >= 1; o >>= 1) {
+      if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) out[C] = red[0];
   }
 }
 
@@ -1613,8 +1660,19 @@ long band_width(long V, long chunk) {
 struct FwdLayout {
   float *pm, *ps, *bsum, *rowloss;
   int* bcnt;
+  float *wpart, *wsum;  // column sums of W by row split, and their total (+ the bias sum)
+  int wsplits;
   size_t bytes;
 };
+
+// Row splits of the column sum of W: enough workgroups to stream W, at most
+// 2^22 partial floats.
+int wsum_splits(long d, long V) {
+  long r = (1L << 22) / (d > 0 ? d : 1);
+  r = r < 1 ? 1 : (r > 64 ? 64 : r);
+  const long rows = ceil_div(V, 256);
+  return (int)(r < rows ? r : (rows > 0 ? rows : 1));
+}
 
 FwdLayout fwd_layout(void* ws, long N, long d, long V, int reduction) {
   Carver c(ws);
@@ -1626,6 +1684,9 @@ FwdLayout fwd_layout(void* ws, long N, long d, long V, int reduction) {
   L.bsum = c.take<float>((size_t)(nb > 0 ? nb : 1));
   L.bcnt = c.take<int>((size_t)(nb > 0 ? nb : 1));
   L.rowloss = (reduction == CCE_REDUCTION_NONE) ? nullptr : c.take<float>((size_t)(N > 0 ? N : 1));
+  L.wsplits = wsum_splits(d, V);
+  L.wpart = c.take<float>((size_t)L.wsplits * d);
+  L.wsum = c.take<float>((size_t)d + 1);
   L.bytes = align_up(c.off, 256);
   return L;
 }
@@ -1878,11 +1939,14 @@ int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_
 
 int cce_forward(const void* hidden, const void* weight, const void* labels, int labels_int64, const float* bias,
                 int64_t N, int64_t d, int64_t V, int64_t ignore_index, float label_smoothing, float z_loss_weight,
-                int reduction, float* loss_out, float* lse_out, int32_t* n_valid_out, void* workspace,
-                size_t workspace_bytes, void* stream) {
+                int smoothing_form, int reduction, float* loss_out, float* lse_out, int32_t* n_valid_out,
+                void* workspace, size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
   int rc = check_dims(N, d, V);
   if (rc) return rc;
+  if (smoothing_form != CCE_SMOOTH_LOGV && smoothing_form != CCE_SMOOTH_UNIFORM)
+    return fail(CCE_ERR_INVALID_ARG, "smoothing_form must be CCE_SMOOTH_LOGV or CCE_SMOOTH_UNIFORM, got %d",
+                smoothing_form);
   if (reduction < CCE_REDUCTION_NONE || reduction > CCE_REDUCTION_SUM)
     return fail(CCE_ERR_INVALID_ARG, "reduction must be 0 (none), 1 (mean) or 2 (sum), got %d", reduction);
   if (!n_valid_out || (!loss_out && !(reduction == CCE_REDUCTION_NONE && N == 0)))
@@ -1928,13 +1992,22 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
               : launch_gemm<kSlowBN, kWarp8, true, true, EpiLse, 3>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE, true);
   if (rc) return rc;
 
+  const bool uniform = smoothing_form == CCE_SMOOTH_UNIFORM && label_smoothing > 0.f;
+  if (uniform) {
+    hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)ceil_div(d, 64), (unsigned)L.wsplits), dim3(256), 0, st,
+                       static_cast<const bf16_t*>(weight), (long)d, (int)V, (int)d, L.wpart);
+    HIP_TRY(hipGetLastError());
+    hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)ceil_div(d, 256)), dim3(256), 0, st, L.wpart, L.wsplits,
+                       (int)d, bias, (int)V, L.wsum);
+    HIP_TRY(hipGetLastError());
+  }
   const int nb = (int)ceil_div(N, 4);
   float* rowloss = (reduction == CCE_REDUCTION_NONE) ? loss_out : L.rowloss;
   const float logV = logf((float)V);
   hipLaunchKernelGGL(fwd_combine_kernel, dim3(nb), dim3(256), 0, st, L.pm, L.ps, S,
                      static_cast<const bf16_t*>(hidden), static_cast<const bf16_t*>(weight), labels, labels_int64,
-                     bias, (int)N, (int)d, (int)V, (long)ignore_index, label_smoothing, z_loss_weight, logV, lse_out,
-                     rowloss, L.bsum, L.bcnt);
+                     bias, (int)N, (int)d, (int)V, (long)ignore_index, label_smoothing, z_loss_weight, logV,
+                     uniform ? L.wsum : nullptr, lse_out, rowloss, L.bsum, L.bcnt);
   HIP_TRY(hipGetLastError());
   hipLaunchKernelGGL(fwd_finalize_kernel, dim3(1), dim3(1024), 0, st, L.bsum, L.bcnt, nb, reduction, loss_out,
                      n_valid_out);

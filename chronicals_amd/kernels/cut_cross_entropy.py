@@ -115,7 +115,8 @@ def _reduction_code(reduction: str) -> int:
         raise ValueError(f"reduction must be 'mean', 'sum' or 'none', got {reduction!r}") from None
 
 
-def _forward_raw(hidden, weight, labels, bias, ignore_index, label_smoothing, z_loss_weight, red):
+def _forward_raw(hidden, weight, labels, bias, ignore_index, label_smoothing, z_loss_weight, red,
+                 smoothing_form=_lib.CCE_SMOOTH_LOGV):
     """Operand preparation + one chronicals_hip::cce_fwd call.
 
     Returns (loss, lse, n_valid, h2, w2, lab, b32): the bf16 [N, d] / [V, d]
@@ -130,7 +131,7 @@ def _forward_raw(hidden, weight, labels, bias, ignore_index, label_smoothing, z_
         lab = lab.contiguous()
     b32 = None if bias is None else bias.detach().to(torch.float32).contiguous()
     loss, lse, n_valid = torch.ops.chronicals_hip.cce_fwd(h2, w2, lab, b32, int(ignore_index), float(label_smoothing),
-                                                          float(z_loss_weight), int(red))
+                                                          float(z_loss_weight), int(smoothing_form), int(red))
     return loss, lse, n_valid, h2, w2, lab, b32
 
 
@@ -157,22 +158,29 @@ class CutCrossEntropyFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output):
-        h2, w2, lab, lse, n_valid, b32 = ctx.saved_tensors
-        chunk_size, ignore_index, eps, zw, red = ctx.cfg
-        hshape, hdtype, wdtype, bdtype = ctx.shapes
-        need_dh = ctx.needs_input_grad[0]
-        need_dw = ctx.needs_input_grad[1]
-        need_db = b32 is not None and ctx.needs_input_grad[3]
-        if not (need_dh or need_dw or need_db):
-            return (None,) * 9
-        # bf16 inputs get bf16 gradients; fp16 / fp32 inputs get them from fp32
-        dh, dw, db = torch.ops.chronicals_hip.cce_bwd(
-            grad_output, h2, w2, lab, lse, n_valid, b32, ignore_index, eps, zw, red, chunk_size,
-            need_dh, need_dw, need_db, hdtype != torch.bfloat16, wdtype != torch.bfloat16)
-        dh = dh.view(hshape).to(hdtype) if need_dh else None
-        dw = dw.to(wdtype) if need_dw else None
-        db = db.to(bdtype) if need_db else None
+        dh, dw, db = _backward_raw(ctx, grad_output, ctx.needs_input_grad[0], ctx.needs_input_grad[1],
+                                   ctx.needs_input_grad[3])
         return dh, dw, None, db, None, None, None, None, None
+
+
+def _backward_raw(ctx, grad_output, need_dh, need_dw, need_db):
+    """One chronicals_hip::cce_bwd call from what _forward_raw's caller saved
+    (ctx.saved_tensors = (h2, w2, lab, lse, n_valid, b32), ctx.cfg, ctx.shapes);
+    returns (dH, dW, dB) in the input dtypes, None where not requested."""
+    h2, w2, lab, lse, n_valid, b32 = ctx.saved_tensors
+    chunk_size, ignore_index, eps, zw, red = ctx.cfg
+    hshape, hdtype, wdtype, bdtype = ctx.shapes
+    need_db = b32 is not None and need_db
+    if not (need_dh or need_dw or need_db):
+        return None, None, None
+    # bf16 inputs get bf16 gradients; fp16 / fp32 inputs get them from fp32
+    dh, dw, db = torch.ops.chronicals_hip.cce_bwd(
+        grad_output, h2, w2, lab, lse, n_valid, b32, ignore_index, eps, zw, red, chunk_size,
+        need_dh, need_dw, need_db, hdtype != torch.bfloat16, wdtype != torch.bfloat16)
+    dh = dh.view(hshape).to(hdtype) if need_dh else None
+    dw = dw.to(wdtype) if need_dw else None
+    db = db.to(bdtype) if need_db else None
+    return dh, dw, db
 
 
 def cut_cross_entropy(

@@ -1,10 +1,11 @@
 """torch.library registration of the fused linear-CE entry points.
 
-Two custom operators wrap the C ABI (include/chronicals_cce.h) so the path is
+Custom operators wrap the C ABI (include/chronicals_cce.h) so the path is
 visible to the PyTorch dispatcher and traceable by ``torch.compile``:
 
   chronicals_hip::cce_fwd(hidden, weight, labels, bias, ignore_index,
-                          label_smoothing, z_loss_weight, reduction)
+                          label_smoothing, z_loss_weight, smoothing_form,
+                          reduction)
       -> (loss, lse, n_valid)
   chronicals_hip::cce_bwd(grad_out, hidden, weight, labels, lse, n_valid, bias,
                           ignore_index, label_smoothing, z_loss_weight,
@@ -20,7 +21,7 @@ backward`` (cut_cross_entropy.py:567, :703).
 Operands: hidden [N, d] and weight [V, d] bf16 and contiguous (a view at an
 unaligned storage offset is copied to 16-byte aligned storage); labels [N]
 int64 or int32; bias fp32 [V] or None; ``reduction`` is a CCE_REDUCTION_*
-code.  Gradients that are not requested come back as empty
+code and ``smoothing_form`` a CCE_SMOOTH_* code.  Gradients that are not requested come back as empty
 tensors.  Only a HIP-device implementation is registered: CPU tensors raise.
 Each fake (meta) implementation gives the output shapes and dtypes without
 touching the device.
@@ -65,7 +66,8 @@ def _check_operands(hidden: Tensor, weight: Tensor, labels: Tensor, bias: Option
 
 @torch.library.custom_op("chronicals_hip::cce_fwd", mutates_args=(), device_types="cuda")
 def cce_fwd(hidden: Tensor, weight: Tensor, labels: Tensor, bias: Optional[Tensor], ignore_index: int,
-            label_smoothing: float, z_loss_weight: float, reduction: int) -> Tuple[Tensor, Tensor, Tensor]:
+            label_smoothing: float, z_loss_weight: float, smoothing_form: int,
+            reduction: int) -> Tuple[Tensor, Tensor, Tensor]:
     _check_operands(hidden, weight, labels, bias)
     hidden, weight = _aligned(hidden), _aligned(weight)
     lib = _lib.load()
@@ -81,14 +83,15 @@ def cce_fwd(hidden: Tensor, weight: Tensor, labels: Tensor, bias: Optional[Tenso
         _lib.check(lib.cce_forward(
             hidden.data_ptr(), weight.data_ptr(), labels.data_ptr(), int(labels.dtype == torch.int64),
             bias.data_ptr() if bias is not None else None,
-            N, d, V, int(ignore_index), float(label_smoothing), float(z_loss_weight), int(reduction),
-            loss.data_ptr(), lse.data_ptr(), n_valid.data_ptr(),
+            N, d, V, int(ignore_index), float(label_smoothing), float(z_loss_weight), int(smoothing_form),
+            int(reduction), loss.data_ptr(), lse.data_ptr(), n_valid.data_ptr(),
             ws.data_ptr(), ws.numel(), _stream(device)))
     return loss, lse, n_valid
 
 
 @cce_fwd.register_fake
-def _cce_fwd_fake(hidden, weight, labels, bias, ignore_index, label_smoothing, z_loss_weight, reduction):
+def _cce_fwd_fake(hidden, weight, labels, bias, ignore_index, label_smoothing, z_loss_weight, smoothing_form,
+                  reduction):
     N = hidden.shape[0]
     loss = hidden.new_empty((N,) if reduction == _lib.CCE_REDUCTION_NONE else (1,), dtype=torch.float32)
     return loss, hidden.new_empty((N,), dtype=torch.float32), hidden.new_empty((1,), dtype=torch.int32)

@@ -75,17 +75,23 @@ int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, 
  * (chronicals/kernels/cut_cross_entropy.py:567-692) plus the reduction of
  * fused_linear_cross_entropy (chronicals/kernels/triton_kernels.py:2481-2491):
  *   lse[n]   = logsumexp_v (hidden[n] . weight[v] + bias[v])         (:627-671)
- *   row[n]   = valid ? (1-eps)*(lse - t) + eps*log(V) + z*lse^2 : 0  (:674-686)
+ *   row[n]   = valid ? (1-eps)*(lse - t) + eps*S + z*lse^2 : 0       (:674-686)
+ *   S        = log(V)                  smoothing_form CCE_SMOOTH_LOGV (:677-679)
+ *            = lse - mean_v(logit[n][v]) CCE_SMOOTH_UNIFORM, the loss of
+ *              triton_fused_linear_cross_entropy (triton_kernels.py:3147-3263
+ *              through _liger_ce_kernel, :2914-2956); the mean is
+ *              hidden[n] . sum_v weight[v] / V (+ mean bias)
  *   loss_out = mean: sum(row)/max(n_valid,1); sum: sum(row); none: row[N]
  *   n_valid_out[0] = number of rows with label != ignore_index        (:618, :689)
  * lse_out [N] fp32 is what cce_backward consumes (the reference saves it at
- * :841).  loss_out holds 1 float (mean/sum) or N floats (none).
+ * :841).  loss_out holds 1 float (mean/sum) or N floats (none).  Both
+ * smoothing forms have the gradient cce_backward computes.
  */
 int cce_forward(const void* hidden, const void* weight, const void* labels, int labels_int64,
                 const float* bias, int64_t N, int64_t d, int64_t V, int64_t ignore_index,
-                float label_smoothing, float z_loss_weight, int reduction, float* loss_out,
-                float* lse_out, int32_t* n_valid_out, void* workspace, size_t workspace_bytes,
-                void* stream);
+                float label_smoothing, float z_loss_weight, int smoothing_form, int reduction,
+                float* loss_out, float* lse_out, int32_t* n_valid_out, void* workspace,
+                size_t workspace_bytes, void* stream);
 
 /* Workspace bytes cce_backward needs (chunk_size = vocabulary band width). */
 int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_size,

@@ -14,7 +14,11 @@ A numpy restatement of the reference's PyTorch CPU algorithm
               label smoothing (1-eps)*ce + eps*log(V) (:677-679),
               z-loss z*lse^2 (:682-683), mask (:686), reductions
               mean = sum/max(n_valid,1) (:688-690) and 'sum'/'none' as in
-              triton_kernels.py:2481-2491.
+              triton_kernels.py:2481-2491.  smoothing='uniform' gives the
+              loss of triton_fused_linear_cross_entropy
+              (triton_kernels.py:3147-3263, whose rows go through
+              _liger_ce_kernel :2914-2956): eps*(lse - mean_v logits)
+              in place of eps*log(V); its gradient is backward()'s.
   backward()  follows CutCrossEntropyBackward.backward, :703-808
               recompute logits per chunk (:762), P = exp(S - lse) (:767),
               G = P - (1-eps)*onehot (:773-780) - eps/V (:783-784)
@@ -73,10 +77,12 @@ def _flat(hidden: np.ndarray, labels: np.ndarray) -> Tuple[np.ndarray, np.ndarra
 def forward(hidden: np.ndarray, weight: np.ndarray, labels: np.ndarray, bias: Optional[np.ndarray] = None,
             chunk_size: int = 8192, ignore_index: int = -100, label_smoothing: float = 0.0,
             z_loss_weight: float = 0.0, use_kahan: bool = True, reduction: str = "mean",
-            dtype=np.float32):
+            dtype=np.float32, smoothing: str = "logv"):
     """Returns (loss, lse [N], target_logit [N], valid_mask [N])."""
     if reduction not in REDUCTIONS:
         raise ValueError(reduction)
+    if smoothing not in ("logv", "uniform"):
+        raise ValueError(smoothing)
     h, lab = _flat(np.asarray(hidden), np.asarray(labels))
     h = h.astype(dtype, copy=False)
     w = np.asarray(weight).astype(dtype, copy=False)
@@ -87,12 +93,15 @@ def forward(hidden: np.ndarray, weight: np.ndarray, labels: np.ndarray, bias: Op
     sum_exp = np.zeros(n, dtype=dtype)
     comp = np.zeros(n, dtype=dtype)
     target = np.zeros(n, dtype=dtype)
+    row_sum = np.zeros(n, dtype=np.float64)
     valid = lab != ignore_index
     for c0 in range(0, V, chunk_size):
         c1 = min(c0 + chunk_size, V)
         logits = h @ w[c0:c1].T
         if b is not None:
             logits = logits + b[c0:c1]
+        if smoothing == "uniform":
+            row_sum += logits.sum(axis=1, dtype=np.float64)
         cmax = logits.max(axis=1) if n else np.zeros(0, dtype)
         new_max = np.maximum(max_logit, cmax)
         sum_exp = sum_exp * np.exp(max_logit - new_max)
@@ -112,7 +121,8 @@ def forward(hidden: np.ndarray, weight: np.ndarray, labels: np.ndarray, bias: Op
     lse = (max_logit + np.log(sum_exp + dtype(1e-10))).astype(dtype)
     ce = lse - target
     if label_smoothing > 0.0:
-        ce = (1.0 - label_smoothing) * ce + label_smoothing * math.log(V)
+        smooth = math.log(V) if smoothing == "logv" else (lse - row_sum / V).astype(dtype)
+        ce = (1.0 - label_smoothing) * ce + label_smoothing * smooth
     total = (ce + z_loss_weight * lse ** 2).astype(dtype)
     total = total * valid.astype(dtype)
     n_valid = max(int(valid.sum()), 1)
@@ -176,10 +186,10 @@ def backward(hidden: np.ndarray, weight: np.ndarray, labels: np.ndarray, lse: np
 
 
 def loss_and_grads(hidden, weight, labels, bias=None, chunk_size=8192, ignore_index=-100, label_smoothing=0.0,
-                   z_loss_weight=0.0, reduction="mean", grad_output=None, dtype=np.float32):
+                   z_loss_weight=0.0, reduction="mean", grad_output=None, dtype=np.float32, smoothing="logv"):
     """forward() then backward() with grad_output (default 1 / ones)."""
     loss, lse, _, valid = forward(hidden, weight, labels, bias, chunk_size, ignore_index, label_smoothing,
-                                  z_loss_weight, True, reduction, dtype)
+                                  z_loss_weight, True, reduction, dtype, smoothing)
     if grad_output is None:
         grad_output = np.ones(np.asarray(labels).size) if reduction == "none" else np.ones(1)
     gh, gw, gb = backward(hidden, weight, labels, lse, valid, grad_output, bias, chunk_size, ignore_index,

@@ -103,7 +103,7 @@ def test_custom_op_fake_shapes_forward(reduction, loss_shape):
         h = torch.empty(300, 128, dtype=torch.bfloat16, device="cuda")
         w = torch.empty(1000, 128, dtype=torch.bfloat16, device="cuda")
         lab = torch.empty(300, dtype=torch.int64, device="cuda")
-        loss, lse, nv = torch.ops.chronicals_hip.cce_fwd(h, w, lab, None, -100, 0.0, 0.0, reduction)
+        loss, lse, nv = torch.ops.chronicals_hip.cce_fwd(h, w, lab, None, -100, 0.0, 0.0, 0, reduction)
         assert tuple(loss.shape) == loss_shape and loss.dtype == torch.float32
         assert tuple(lse.shape) == (300,) and lse.dtype == torch.float32
         assert tuple(nv.shape) == (1,) and nv.dtype == torch.int32
@@ -135,7 +135,7 @@ def test_custom_op_has_no_cpu_kernel():
     import chronicals_amd.ops  # noqa: F401
     with pytest.raises(NotImplementedError):
         torch.ops.chronicals_hip.cce_fwd(torch.zeros(4, 8, dtype=torch.bfloat16), torch.zeros(5, 8, dtype=torch.bfloat16),
-                                         torch.zeros(4, dtype=torch.int64), None, -100, 0.0, 0.0, 1)
+                                         torch.zeros(4, dtype=torch.int64), None, -100, 0.0, 0.0, 0, 1)
 
 
 # ---------------------------------------------------------------------------
@@ -198,3 +198,51 @@ def test_logits_ops_have_no_cpu_kernel():
     with pytest.raises(NotImplementedError):
         torch.ops.chronicals_hip.ce_logits_fwd(torch.zeros(4, 8), torch.zeros(4, dtype=torch.int64), -100, 0.0, 0.0,
                                                0, 1)
+
+
+# ---------------------------------------------------------------------------
+# Sibling fused linear-CE APIs (chronicals_amd/kernels/fused_linear_cross_entropy.py)
+# ---------------------------------------------------------------------------
+
+def test_fused_linear_api_signatures_match_reference():
+    from chronicals_amd.kernels import fused_linear_cross_entropy as fl
+    sig = lambda f: list(inspect.signature(f).parameters)  # noqa: E731
+    # triton_kernels.py:2308-2315, :2398-2408, :2636-2645, :2659-2666
+    assert sig(fl.fused_linear_cross_entropy_forward) == ["hidden", "weight", "labels", "bias", "chunk_size",
+                                                          "ignore_index"]
+    assert sig(fl.fused_linear_cross_entropy) == ["hidden", "weight", "labels", "bias", "label_smoothing",
+                                                  "z_loss_weight", "ignore_index", "chunk_size", "reduction"]
+    assert sig(fl.fused_linear_cross_entropy_autograd) == ["hidden", "weight", "labels", "bias", "label_smoothing",
+                                                           "z_loss_weight", "ignore_index", "chunk_size"]
+    assert sig(fl.chunked_cross_entropy) == ["logits", "labels", "chunk_size", "label_smoothing", "z_loss_weight",
+                                             "ignore_index"]
+    assert inspect.signature(fl.fused_linear_cross_entropy).parameters["z_loss_weight"].default == 1e-4
+    assert inspect.signature(fl.chunked_cross_entropy).parameters["z_loss_weight"].default == 1e-4
+    # :3147-3157, :3318-3328
+    for f in (fl.triton_fused_linear_cross_entropy_forward, fl.triton_fused_linear_cross_entropy):
+        assert sig(f) == ["hidden", "weight", "target", "bias", "ignore_index", "lse_square_scale",
+                          "label_smoothing", "reduction", "chunk_size"]
+    assert sig(fl.FusedLinearCrossEntropyLoss.forward) == ["self", "hidden", "weight", "bias", "labels"]
+    assert sig(fl.TritonFusedLinearCrossEntropyLoss.forward) == ["self", "hidden", "weight", "target", "bias"]
+    m = fl.FusedLinearCrossEntropyLoss()
+    assert (m.chunk_size, m.label_smoothing, m.z_loss_weight, m.ignore_index) == (8192, 0.0, 1e-4, -100)
+    t = fl.TritonFusedLinearCrossEntropyLoss()
+    assert (t.chunk_size, t.ignore_index, t.lse_square_scale, t.label_smoothing, t.reduction) == (
+        8192, -100, 0.0, 0.0, "mean")
+    assert fl.ChunkedCrossEntropyLoss is fl.FusedLinearCrossEntropyLoss
+    assert fl.LigerFusedLinearCrossEntropyLoss is fl.TritonFusedLinearCrossEntropyLoss
+    assert fl.DEFAULT_CHUNK_SIZE == 8192
+
+
+def test_fused_linear_apis_refuse_cpu_tensors():
+    from chronicals_amd.kernels import fused_linear_cross_entropy as fl
+    h, w, lab = torch.randn(4, 8), torch.randn(10, 8), torch.zeros(4, dtype=torch.long)
+    for call in (lambda: fl.fused_linear_cross_entropy(h, w, lab),
+                 lambda: fl.fused_linear_cross_entropy_autograd(h, w, lab),
+                 lambda: fl.FusedLinearCrossEntropyLoss()(h, w, None, lab),
+                 lambda: fl.triton_fused_linear_cross_entropy(h, w, lab),
+                 lambda: fl.triton_fused_linear_cross_entropy_forward(h, w, lab),
+                 lambda: fl.fused_linear_cross_entropy_forward(h, w, lab),
+                 lambda: fl.chunked_cross_entropy(torch.randn(1, 4, 10), lab.view(1, 4))):
+        with pytest.raises(RuntimeError, match="HIP devices"):
+            call()

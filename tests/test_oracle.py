@@ -193,3 +193,43 @@ def test_planted_reference_bug_is_rejected():
         np.testing.assert_allclose(gh, ref["dh"].numpy(), rtol=1e-3, atol=1e-5)
     with pytest.raises(AssertionError):
         np.testing.assert_allclose(gw, ref["dw"].numpy(), rtol=1e-3, atol=1e-5)
+
+
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+def test_oracle_uniform_smoothing_is_torch_label_smoothed_cross_entropy(bias, reduction):
+    # the loss of triton_fused_linear_cross_entropy (_liger_ce_kernel, triton_kernels.py:2914-2956) is torch's
+    # label-smoothed cross-entropy of the logits plus z*lse^2; the oracle forms the row mean of the logits per chunk
+    h, w, lab, b = _case(N=33, d=24, V=777, seed=8, bias=bias)
+    eps, z = 0.2, 1e-3
+    logits = h.double() @ w.double().t() + (b.double() if bias else 0.0)
+    rows = F.cross_entropy(logits, lab, ignore_index=IGNORE, label_smoothing=eps, reduction="none")
+    rows = (rows + z * torch.logsumexp(logits, -1) ** 2) * (lab != IGNORE).double()
+    nv = max(int((lab != IGNORE).sum()), 1)
+    ref = {"mean": rows.sum() / nv, "sum": rows.sum(), "none": rows}[reduction].numpy()
+    for chunk in (100, 8192):
+        loss, *_ = oracle.forward(_np(h), _np(w), _np(lab), _np(b), chunk_size=chunk, label_smoothing=eps,
+                                  z_loss_weight=z, reduction=reduction, dtype=np.float64, smoothing="uniform")
+        np.testing.assert_allclose(loss, ref, rtol=1e-9, atol=1e-12)
+    # the eps*log(V) form differs from it whenever eps > 0 (the check tells the two apart)
+    lv, *_ = oracle.forward(_np(h), _np(w), _np(lab), _np(b), label_smoothing=eps, z_loss_weight=z,
+                            reduction="sum", dtype=np.float64)
+    assert abs(float(lv) - float(rows.sum())) > 1e-3
+
+
+def test_oracle_uniform_smoothing_gradient_is_its_autograd():
+    # backward()'s P - (1-eps)onehot - eps/V + 2z*lse*P is the exact derivative of the uniform-form loss
+    h, w, lab, b = _case(N=21, d=16, V=301, seed=9, bias=True)
+    eps, z = 0.15, 1e-2
+    hd = h.double().requires_grad_(True)
+    wd = w.double().requires_grad_(True)
+    bd = b.double().requires_grad_(True)
+    logits = hd @ wd.t() + bd
+    rows = F.cross_entropy(logits, lab, ignore_index=IGNORE, label_smoothing=eps, reduction="none")
+    rows = (rows + z * torch.logsumexp(logits, -1) ** 2) * (lab != IGNORE).double()
+    (rows.sum() / max(int((lab != IGNORE).sum()), 1)).backward()
+    loss, lse, gh, gw, gb = oracle.loss_and_grads(_np(h), _np(w), _np(lab), _np(b), chunk_size=64, label_smoothing=eps,
+                                                  z_loss_weight=z, dtype=np.float64, smoothing="uniform")
+    np.testing.assert_allclose(gh, hd.grad.numpy(), rtol=1e-8, atol=1e-13)
+    np.testing.assert_allclose(gw, wd.grad.numpy(), rtol=1e-8, atol=1e-13)
+    np.testing.assert_allclose(gb, bd.grad.numpy(), rtol=1e-8, atol=1e-13)
