@@ -56,7 +56,7 @@ SIGNATURES = {
         _vp, _vp, _vp, _i32, _vp,            # hidden, weight, labels, labels_int64, bias
         _i64, _i64, _i64, _i64,              # N, d, V, ignore_index
         _f32, _f32, _i32, _i32,              # label_smoothing, z_loss_weight, smoothing_form, reduction
-        _vp, _vp, _vp,                       # loss_out, lse_out, n_valid_out
+        _vp, _vp, _vp, _vp,                  # loss_out, lse_out, target_out, n_valid_out
         _vp, _sz, _vp,                       # workspace, workspace_bytes, stream
     ]),
     "cce_backward": (_i32, [

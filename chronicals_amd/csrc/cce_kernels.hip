@@ -1137,7 +1137,8 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(
     const float* __restrict__ pm, const float* __restrict__ ps, int splits, const bf16_t* __restrict__ H,
     const bf16_t* __restrict__ W, const void* labels, int labels64, const float* __restrict__ bias, int N, int d,
     int V, long ignore_index, float eps, float zw, float logV, const float* __restrict__ wsum,
-    float* __restrict__ lse_out, float* __restrict__ rowloss, float* __restrict__ bsum, int* __restrict__ bcnt) {
+    float* __restrict__ lse_out, float* __restrict__ target_out, float* __restrict__ rowloss,
+    float* __restrict__ bsum, int* __restrict__ bcnt) {
   const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int n = blockIdx.x * 4 + w;
   __shared__ float s_loss[4];
@@ -1207,6 +1208,7 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(
     if (l == 0) {
       lse_out[n] = lse;
       rowloss[n] = loss;
+      if (target_out) target_out[n] = t;
     }
   }
   if (l == 0) {
@@ -1939,8 +1941,8 @@ int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_
 
 int cce_forward(const void* hidden, const void* weight, const void* labels, int labels_int64, const float* bias,
                 int64_t N, int64_t d, int64_t V, int64_t ignore_index, float label_smoothing, float z_loss_weight,
-                int smoothing_form, int reduction, float* loss_out, float* lse_out, int32_t* n_valid_out,
-                void* workspace, size_t workspace_bytes, void* stream) {
+                int smoothing_form, int reduction, float* loss_out, float* lse_out, float* target_out,
+                int32_t* n_valid_out, void* workspace, size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
   int rc = check_dims(N, d, V);
   if (rc) return rc;
@@ -2007,7 +2009,7 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
   hipLaunchKernelGGL(fwd_combine_kernel, dim3(nb), dim3(256), 0, st, L.pm, L.ps, S,
                      static_cast<const bf16_t*>(hidden), static_cast<const bf16_t*>(weight), labels, labels_int64,
                      bias, (int)N, (int)d, (int)V, (long)ignore_index, label_smoothing, z_loss_weight, logV,
-                     uniform ? L.wsum : nullptr, lse_out, rowloss, L.bsum, L.bcnt);
+                     uniform ? L.wsum : nullptr, lse_out, target_out, rowloss, L.bsum, L.bcnt);
   HIP_TRY(hipGetLastError());
   hipLaunchKernelGGL(fwd_finalize_kernel, dim3(1), dim3(1024), 0, st, L.bsum, L.bcnt, nb, reduction, loss_out,
                      n_valid_out);

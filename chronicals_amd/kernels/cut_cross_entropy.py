@@ -46,6 +46,9 @@ __all__ = [
     "ChunkedCrossEntropyLoss",
     "CutCrossEntropyLoss",
     "CutCrossEntropyFunction",
+    "CutCrossEntropyForward",
+    "CutCrossEntropyBackward",
+    "AdaptiveCrossEntropyLoss",
     "get_optimal_chunk_size",
     "estimate_memory_savings",
     "compute_z_loss",
@@ -119,8 +122,9 @@ def _forward_raw(hidden, weight, labels, bias, ignore_index, label_smoothing, z_
                  smoothing_form=_lib.CCE_SMOOTH_LOGV):
     """Operand preparation + one chronicals_hip::cce_fwd call.
 
-    Returns (loss, lse, n_valid, h2, w2, lab, b32): the bf16 [N, d] / [V, d]
-    operands, flat labels and fp32 bias the backward reuses.
+    Returns (loss, lse, n_valid, h2, w2, lab, b32, target): the bf16 [N, d] /
+    [V, d] operands, flat labels and fp32 bias the backward reuses, and the
+    per-row target logits.
     """
     _validate(hidden, weight, labels, bias)
     d = hidden.shape[-1]
@@ -130,9 +134,10 @@ def _forward_raw(hidden, weight, labels, bias, ignore_index, label_smoothing, z_
     if not lab.is_contiguous():
         lab = lab.contiguous()
     b32 = None if bias is None else bias.detach().to(torch.float32).contiguous()
-    loss, lse, n_valid = torch.ops.chronicals_hip.cce_fwd(h2, w2, lab, b32, int(ignore_index), float(label_smoothing),
-                                                          float(z_loss_weight), int(smoothing_form), int(red))
-    return loss, lse, n_valid, h2, w2, lab, b32
+    loss, lse, n_valid, target = torch.ops.chronicals_hip.cce_fwd(h2, w2, lab, b32, int(ignore_index),
+                                                                  float(label_smoothing), float(z_loss_weight),
+                                                                  int(smoothing_form), int(red))
+    return loss, lse, n_valid, h2, w2, lab, b32, target
 
 
 class CutCrossEntropyFunction(torch.autograd.Function):
@@ -147,8 +152,8 @@ class CutCrossEntropyFunction(torch.autograd.Function):
     def forward(ctx, hidden, weight, labels, bias, chunk_size, ignore_index, label_smoothing, z_loss_weight,
                 reduction="mean"):
         red = _reduction_code(reduction)
-        loss, lse, n_valid, h2, w2, lab, b32 = _forward_raw(hidden, weight, labels, bias, ignore_index,
-                                                            label_smoothing, z_loss_weight, red)
+        loss, lse, n_valid, h2, w2, lab, b32, _ = _forward_raw(hidden, weight, labels, bias, ignore_index,
+                                                               label_smoothing, z_loss_weight, red)
         ctx.save_for_backward(h2, w2, lab, lse, n_valid, b32)
         ctx.cfg = (int(chunk_size), int(ignore_index), float(label_smoothing), float(z_loss_weight), red)
         ctx.shapes = (hidden.shape, hidden.dtype, weight.dtype, None if bias is None else bias.dtype)
@@ -181,6 +186,89 @@ def _backward_raw(ctx, grad_output, need_dh, need_dw, need_db):
     dw = dw.to(wdtype) if need_dw else None
     db = db.to(bdtype) if need_db else None
     return dh, dw, db
+
+
+class _LinearCE(torch.autograd.Function):
+    """(loss, lse) of the fused kernels; lse carries no gradient.
+
+    apply(hidden, weight, labels, bias, chunk_size, ignore_index, eps, z,
+          reduction_code, smoothing_form)
+    """
+
+    @staticmethod
+    def forward(ctx, hidden, weight, labels, bias, chunk_size, ignore_index, eps, z, red, form):
+        loss, lse, n_valid, h2, w2, lab, b32, _ = _forward_raw(hidden, weight, labels, bias, ignore_index, eps, z, red,
+                                                            form)
+        ctx.save_for_backward(h2, w2, lab, lse, n_valid, b32)
+        ctx.cfg = (int(chunk_size), int(ignore_index), float(eps), float(z), red)
+        ctx.shapes = (hidden.shape, hidden.dtype, weight.dtype, None if bias is None else bias.dtype)
+        ctx.mark_non_differentiable(lse)
+        out = loss.view(labels.shape) if red == _lib.CCE_REDUCTION_NONE else loss.view(())
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, grad_loss, grad_lse):
+        del grad_lse
+        dh, dw, db = _backward_raw(ctx, grad_loss, ctx.needs_input_grad[0], ctx.needs_input_grad[1],
+                                   ctx.needs_input_grad[3])
+        return dh, dw, None, db, None, None, None, None, None, None
+
+
+class CutCrossEntropyForward:
+    """The reference's forward pass as a static method (cut_cross_entropy.py:559-692), on cce_forward."""
+
+    @staticmethod
+    def forward(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                chunk_size: int = 8192, ignore_index: int = -100, label_smoothing: float = 0.0,
+                z_loss_weight: float = 0.0, use_kahan: bool = True):
+        """(loss, logsumexp [N], target_logit [N], valid_mask [N]); 'mean' loss, no autograd.
+        ``use_kahan`` is accepted: the kernels merge fp32 partials in a fixed order."""
+        del chunk_size, use_kahan
+        with torch.no_grad():
+            loss, lse, _, _, _, lab, _, target = _forward_raw(hidden, weight, labels, bias, ignore_index,
+                                                              label_smoothing, z_loss_weight,
+                                                              _lib.CCE_REDUCTION_MEAN)
+        return loss.view(()), lse, target, lab != ignore_index
+
+
+class CutCrossEntropyBackward:
+    """The reference's backward pass as a static method (cut_cross_entropy.py:695-808), on cce_backward."""
+
+    @staticmethod
+    def backward(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor, logsumexp: torch.Tensor,
+                 valid_mask: torch.Tensor, grad_output: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                 chunk_size: int = 8192, ignore_index: int = -100, label_smoothing: float = 0.0,
+                 z_loss_weight: float = 0.0):
+        """(grad_hidden, grad_weight, grad_bias or None) of the 'mean' loss times grad_output.
+
+        Rows where ``valid_mask`` is False are treated as ignored.  A scalar
+        grad_output scales every row by grad_output / n_valid; a per-row one
+        scales row n by grad_output[n] / n_valid (:745).  The one-hot term is
+        applied (the reference's CPU path loses it at :773-780).
+        """
+        _validate(hidden, weight, labels, bias)
+        d = hidden.shape[-1]
+        with torch.no_grad():
+            h2 = _as_bf16_rows(hidden.detach().reshape(-1, d))
+            w2 = _as_bf16_rows(weight.detach())
+            vm = valid_mask.reshape(-1).to(torch.bool)
+            lab = torch.where(vm, labels.reshape(-1).to(torch.int64),
+                              torch.full_like(vm, int(ignore_index), dtype=torch.int64)).contiguous()
+            n_valid = vm.sum().to(torch.int32).reshape(1)
+            b32 = None if bias is None else bias.detach().to(torch.float32).contiguous()
+            lse = logsumexp.detach().reshape(-1).to(torch.float32).contiguous()
+            g = torch.as_tensor(grad_output, device=h2.device).detach().to(torch.float32)
+            if g.numel() == 1:
+                red = _lib.CCE_REDUCTION_MEAN
+            else:
+                red = _lib.CCE_REDUCTION_NONE
+                g = g.reshape(-1) / n_valid.clamp(min=1).to(torch.float32)
+            dh, dw, db = torch.ops.chronicals_hip.cce_bwd(
+                g, h2, w2, lab, lse, n_valid, b32, int(ignore_index), float(label_smoothing), float(z_loss_weight),
+                red, int(chunk_size), True, True, b32 is not None, hidden.dtype != torch.bfloat16,
+                weight.dtype != torch.bfloat16)
+        return (dh.view(hidden.shape).to(hidden.dtype), dw.to(weight.dtype),
+                db.to(bias.dtype) if bias is not None else None)
 
 
 def cut_cross_entropy(
@@ -242,6 +330,50 @@ class CutCrossEntropyLoss(nn.Module):
                 f"label_smoothing={self.label_smoothing}, z_loss_weight={self.z_loss_weight}")
 
 
+class AdaptiveCrossEntropyLoss(nn.Module):
+    """Picks the cross-entropy form by vocabulary size (reference cut_cross_entropy.py:1283-1372).
+
+    forward(hidden, weight, labels, bias=None) or forward(logits, labels).
+    Below ``small_vocab_threshold`` the reference uses torch's
+    nn.CrossEntropyLoss (uniform-target label smoothing, no z-loss, mean over
+    the non-ignored rows); at or above it, CutCrossEntropyLoss (hidden) or
+    chunked_cross_entropy_loss (logits).  Every branch runs on the HIP
+    kernels: the small-vocabulary ones with the uniform smoothing form and
+    z = 0.  With every label ignored the small-vocabulary branches return 0
+    (torch's mean is NaN there).
+    """
+
+    def __init__(self, small_vocab_threshold: int = 32000, large_vocab_threshold: int = 100000,
+                 ignore_index: int = -100, label_smoothing: float = 0.0, z_loss_weight: float = 0.0):
+        super().__init__()
+        self.small_vocab_threshold = small_vocab_threshold
+        self.large_vocab_threshold = large_vocab_threshold
+        self.ignore_index = ignore_index
+        self.label_smoothing = label_smoothing
+        self.z_loss_weight = z_loss_weight
+        self.cce = CutCrossEntropyLoss(ignore_index=ignore_index, label_smoothing=label_smoothing,
+                                       z_loss_weight=z_loss_weight)
+
+    def forward(self, hidden_or_logits: torch.Tensor, weight_or_labels: torch.Tensor,
+                labels_or_none: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+        from .logits_cross_entropy import LogitsCrossEntropyFunction, _rows
+        if labels_or_none is not None:
+            hidden, weight, labels = hidden_or_logits, weight_or_labels, labels_or_none
+            if weight.shape[0] < self.small_vocab_threshold:
+                loss, _ = _LinearCE.apply(hidden, weight, labels, bias, 8192, self.ignore_index,
+                                          self.label_smoothing, 0.0, _lib.CCE_REDUCTION_MEAN,
+                                          _lib.CCE_SMOOTH_UNIFORM)
+                return loss
+            return self.cce(hidden, weight, labels, bias)
+        logits, labels = hidden_or_logits, weight_or_labels
+        if logits.shape[-1] < self.small_vocab_threshold:
+            x, lab = _rows(logits, labels, "AdaptiveCrossEntropyLoss")
+            return LogitsCrossEntropyFunction.apply(x, lab, self.ignore_index, self.label_smoothing, 0.0,
+                                                    _lib.CCE_SMOOTH_UNIFORM, _lib.CCE_REDUCTION_MEAN)
+        return chunked_cross_entropy_loss(logits, labels, ignore_index=self.ignore_index,
+                                          label_smoothing=self.label_smoothing, z_loss_weight=self.z_loss_weight)
+
+
 def compute_z_loss(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
                    bias: Optional[torch.Tensor] = None, ignore_index: int = -100,
                    chunk_size: int = 8192) -> torch.Tensor:
@@ -251,8 +383,8 @@ def compute_z_loss(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Ten
     pass only).  ``chunk_size`` is accepted for signature compatibility.
     """
     del chunk_size
-    _, lse, _, _, _, lab, _ = _forward_raw(hidden, weight, labels, bias, ignore_index, 0.0, 0.0,
-                                           _lib.CCE_REDUCTION_NONE)
+    _, lse, _, _, _, lab, _, _ = _forward_raw(hidden, weight, labels, bias, ignore_index, 0.0, 0.0,
+                                              _lib.CCE_REDUCTION_MEAN)
     valid = (lab != ignore_index).to(torch.float32)
     return (lse * lse * valid).sum() / valid.sum().clamp(min=1)
 

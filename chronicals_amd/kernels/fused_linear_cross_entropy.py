@@ -42,7 +42,7 @@ import torch
 import torch.nn as nn
 
 from .. import _lib
-from .cut_cross_entropy import _backward_raw, _forward_raw, _reduction_code
+from .cut_cross_entropy import _backward_raw, _forward_raw, _LinearCE, _reduction_code
 from .logits_cross_entropy import LogitsCrossEntropyFunction, _rows
 
 DEFAULT_CHUNK_SIZE = 8192  # reference triton_kernels.py:2297
@@ -62,32 +62,6 @@ __all__ = [
     "TritonFusedLinearCrossEntropyLoss",
     "LigerFusedLinearCrossEntropyLoss",
 ]
-
-
-class _LinearCE(torch.autograd.Function):
-    """(loss, lse) of the fused kernels; lse carries no gradient.
-
-    apply(hidden, weight, labels, bias, chunk_size, ignore_index, eps, z,
-          reduction_code, smoothing_form)
-    """
-
-    @staticmethod
-    def forward(ctx, hidden, weight, labels, bias, chunk_size, ignore_index, eps, z, red, form):
-        loss, lse, n_valid, h2, w2, lab, b32 = _forward_raw(hidden, weight, labels, bias, ignore_index, eps, z, red,
-                                                            form)
-        ctx.save_for_backward(h2, w2, lab, lse, n_valid, b32)
-        ctx.cfg = (int(chunk_size), int(ignore_index), float(eps), float(z), red)
-        ctx.shapes = (hidden.shape, hidden.dtype, weight.dtype, None if bias is None else bias.dtype)
-        ctx.mark_non_differentiable(lse)
-        out = loss.view(labels.shape) if red == _lib.CCE_REDUCTION_NONE else loss.view(())
-        return out, lse
-
-    @staticmethod
-    def backward(ctx, grad_loss, grad_lse):
-        del grad_lse
-        dh, dw, db = _backward_raw(ctx, grad_loss, ctx.needs_input_grad[0], ctx.needs_input_grad[1],
-                                   ctx.needs_input_grad[3])
-        return dh, dw, None, db, None, None, None, None, None, None
 
 
 def _z_loss(lse: torch.Tensor, labels: torch.Tensor, ignore_index: int, z: float, red: int) -> torch.Tensor:
@@ -120,12 +94,9 @@ def fused_linear_cross_entropy_forward(
     """
     del chunk_size
     with torch.no_grad():
-        rows, lse = _LinearCE.apply(hidden, weight, labels, bias, DEFAULT_CHUNK_SIZE, ignore_index, 0.0, 0.0,
-                                    _lib.CCE_REDUCTION_NONE, _lib.CCE_SMOOTH_LOGV)
-    lab = labels.reshape(-1)
-    valid = lab != ignore_index
-    target = torch.where(valid, lse - rows.reshape(-1), torch.zeros_like(lse))
-    return lse, target, valid
+        _, lse, _, _, _, lab, _, target = _forward_raw(hidden, weight, labels, bias, ignore_index, 0.0, 0.0,
+                                                       _lib.CCE_REDUCTION_MEAN)
+    return lse, target, lab != ignore_index
 
 
 def fused_linear_cross_entropy(
@@ -161,7 +132,7 @@ class FusedLinearCrossEntropyFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden, weight, bias, labels, label_smoothing, z_loss_weight, ignore_index, chunk_size):
         red = _lib.CCE_REDUCTION_MEAN
-        loss, lse, n_valid, h2, w2, lab, b32 = _forward_raw(hidden, weight, labels, bias, ignore_index,
+        loss, lse, n_valid, h2, w2, lab, b32, _ = _forward_raw(hidden, weight, labels, bias, ignore_index,
                                                             label_smoothing, z_loss_weight, red)
         ctx.save_for_backward(h2, w2, lab, lse, n_valid, b32)
         ctx.cfg = (int(chunk_size), int(ignore_index), float(label_smoothing), float(z_loss_weight), red)
@@ -260,7 +231,7 @@ def triton_fused_linear_cross_entropy_forward(
     need_dw = bool(weight.requires_grad)
     need_db = bias is not None and bool(bias.requires_grad)
     with torch.no_grad():
-        loss, lse, n_valid, h2, w2, lab, b32 = _forward_raw(hidden, weight, target, bias, ignore_index,
+        loss, lse, n_valid, h2, w2, lab, b32, _ = _forward_raw(hidden, weight, target, bias, ignore_index,
                                                             label_smoothing, lse_square_scale, red,
                                                             _lib.CCE_SMOOTH_UNIFORM)
         gred = _lib.CCE_REDUCTION_SUM if red == _lib.CCE_REDUCTION_NONE else red
@@ -287,7 +258,7 @@ class TritonFusedLinearCrossEntropyFunction(torch.autograd.Function):
     def forward(ctx, hidden, weight, target, bias=None, ignore_index=-100, lse_scale=0.0, label_smoothing=0.0,
                 reduction="mean", chunk_size=8192):
         red = _reduction_code(reduction)
-        loss, lse, n_valid, h2, w2, lab, b32 = _forward_raw(hidden, weight, target, bias, ignore_index,
+        loss, lse, n_valid, h2, w2, lab, b32, _ = _forward_raw(hidden, weight, target, bias, ignore_index,
                                                             label_smoothing, lse_scale, red,
                                                             _lib.CCE_SMOOTH_UNIFORM)
         ctx.save_for_backward(h2, w2, lab, lse, n_valid, b32)

@@ -6,7 +6,7 @@ visible to the PyTorch dispatcher and traceable by ``torch.compile``:
   chronicals_hip::cce_fwd(hidden, weight, labels, bias, ignore_index,
                           label_smoothing, z_loss_weight, smoothing_form,
                           reduction)
-      -> (loss, lse, n_valid)
+      -> (loss, lse, n_valid, target_logit)
   chronicals_hip::cce_bwd(grad_out, hidden, weight, labels, lse, n_valid, bias,
                           ignore_index, label_smoothing, z_loss_weight,
                           reduction, chunk_size, need_dh, need_dw, need_db,
@@ -67,7 +67,7 @@ def _check_operands(hidden: Tensor, weight: Tensor, labels: Tensor, bias: Option
 @torch.library.custom_op("chronicals_hip::cce_fwd", mutates_args=(), device_types="cuda")
 def cce_fwd(hidden: Tensor, weight: Tensor, labels: Tensor, bias: Optional[Tensor], ignore_index: int,
             label_smoothing: float, z_loss_weight: float, smoothing_form: int,
-            reduction: int) -> Tuple[Tensor, Tensor, Tensor]:
+            reduction: int) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
     _check_operands(hidden, weight, labels, bias)
     hidden, weight = _aligned(hidden), _aligned(weight)
     lib = _lib.load()
@@ -79,14 +79,15 @@ def cce_fwd(hidden: Tensor, weight: Tensor, labels: Tensor, bias: Optional[Tenso
         loss = torch.empty((N,) if reduction == _lib.CCE_REDUCTION_NONE else (1,), dtype=torch.float32,
                            device=device)
         lse = torch.empty((N,), dtype=torch.float32, device=device)
+        target = torch.empty((N,), dtype=torch.float32, device=device)
         n_valid = torch.empty((1,), dtype=torch.int32, device=device)
         _lib.check(lib.cce_forward(
             hidden.data_ptr(), weight.data_ptr(), labels.data_ptr(), int(labels.dtype == torch.int64),
             bias.data_ptr() if bias is not None else None,
             N, d, V, int(ignore_index), float(label_smoothing), float(z_loss_weight), int(smoothing_form),
-            int(reduction), loss.data_ptr(), lse.data_ptr(), n_valid.data_ptr(),
+            int(reduction), loss.data_ptr(), lse.data_ptr(), target.data_ptr(), n_valid.data_ptr(),
             ws.data_ptr(), ws.numel(), _stream(device)))
-    return loss, lse, n_valid
+    return loss, lse, n_valid, target
 
 
 @cce_fwd.register_fake
@@ -94,7 +95,8 @@ def _cce_fwd_fake(hidden, weight, labels, bias, ignore_index, label_smoothing, z
                   reduction):
     N = hidden.shape[0]
     loss = hidden.new_empty((N,) if reduction == _lib.CCE_REDUCTION_NONE else (1,), dtype=torch.float32)
-    return loss, hidden.new_empty((N,), dtype=torch.float32), hidden.new_empty((1,), dtype=torch.int32)
+    return (loss, hidden.new_empty((N,), dtype=torch.float32), hidden.new_empty((1,), dtype=torch.int32),
+            hidden.new_empty((N,), dtype=torch.float32))
 
 
 @torch.library.custom_op("chronicals_hip::cce_bwd", mutates_args=(), device_types="cuda")

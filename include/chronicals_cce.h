@@ -83,6 +83,8 @@ int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, 
  *              hidden[n] . sum_v weight[v] / V (+ mean bias)
  *   loss_out = mean: sum(row)/max(n_valid,1); sum: sum(row); none: row[N]
  *   n_valid_out[0] = number of rows with label != ignore_index        (:618, :689)
+ *   target_out[n] = hidden[n] . weight[label] + bias[label], 0 for ignored rows
+ *                   and labels outside [0, V) (:663-668); may be NULL
  * lse_out [N] fp32 is what cce_backward consumes (the reference saves it at
  * :841).  loss_out holds 1 float (mean/sum) or N floats (none).  Both
  * smoothing forms have the gradient cce_backward computes.
@@ -90,8 +92,8 @@ int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, 
 int cce_forward(const void* hidden, const void* weight, const void* labels, int labels_int64,
                 const float* bias, int64_t N, int64_t d, int64_t V, int64_t ignore_index,
                 float label_smoothing, float z_loss_weight, int smoothing_form, int reduction,
-                float* loss_out, float* lse_out, int32_t* n_valid_out, void* workspace,
-                size_t workspace_bytes, void* stream);
+                float* loss_out, float* lse_out, float* target_out, int32_t* n_valid_out,
+                void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes cce_backward needs (chunk_size = vocabulary band width). */
 int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_size,

@@ -132,21 +132,21 @@ def test_workspace_query_rejects_bad_arguments(lib, N, d, V, red, msg):
 def test_forward_rejects_small_workspace_before_launch(lib):
     fake = 0x10000  # never dereferenced: validation fails first
     rc = lib.cce_forward(fake, fake, fake, 1, None, 64, 64, 1000, -100, 0.0, 0.0, _lib.CCE_SMOOTH_LOGV,
-                         _lib.CCE_REDUCTION_MEAN, fake, fake, fake, fake, 16, None)
+                         _lib.CCE_REDUCTION_MEAN, fake, fake, None, fake, fake, 16, None)
     assert rc == _lib.CCE_ERR_WORKSPACE
     assert "workspace too small" in lib.cce_last_error().decode()
 
 
 def test_forward_rejects_null_inputs(lib):
     rc = lib.cce_forward(None, None, None, 1, None, 64, 64, 1000, -100, 0.0, 0.0, _lib.CCE_SMOOTH_LOGV,
-                         _lib.CCE_REDUCTION_MEAN, 0x10000, 0x10000, 0x10000, 0x10000, 1 << 20, None)
+                         _lib.CCE_REDUCTION_MEAN, 0x10000, 0x10000, None, 0x10000, 0x10000, 1 << 20, None)
     assert rc == _lib.CCE_ERR_INVALID_ARG
 
 
 def test_forward_rejects_bad_smoothing_form(lib):
     fake = 0x10000
     rc = lib.cce_forward(fake, fake, fake, 1, None, 64, 64, 1000, -100, 0.1, 0.0, 2, _lib.CCE_REDUCTION_MEAN,
-                         fake, fake, fake, fake, 1 << 30, None)
+                         fake, fake, None, fake, fake, 1 << 30, None)
     assert rc == _lib.CCE_ERR_INVALID_ARG and "smoothing_form" in lib.cce_last_error().decode()
     rc = lib.cce_logits_forward(fake, 0, 1000, fake, 1, 64, 1000, -100, 0.1, 0.0, 5, 1, fake, fake, fake, fake,
                                 1 << 30, None)
@@ -165,7 +165,7 @@ def test_backward_rejects_bad_dtype_and_bias(lib):
 
 def test_misaligned_pointers_rejected(lib):
     rc = lib.cce_forward(0x10002, 0x10000, 0x10000, 1, None, 64, 64, 1000, -100, 0.0, 0.0, 0, 1,
-                         0x10000, 0x10000, 0x10000, 0x10000, 1 << 20, None)
+                         0x10000, 0x10000, None, 0x10000, 0x10000, 1 << 20, None)
     assert rc == _lib.CCE_ERR_INVALID_ARG and "aligned" in lib.cce_last_error().decode()
 
 

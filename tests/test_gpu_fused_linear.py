@@ -1,4 +1,6 @@
-"""GPU parity of the sibling fused linear-CE APIs (chronicals_amd.kernels.fused_linear_cross_entropy).
+"""GPU parity of the sibling fused linear-CE APIs (chronicals_amd.kernels.fused_linear_cross_entropy)
+and of the remaining public classes of the drop-in module (CutCrossEntropyForward /
+CutCrossEntropyBackward, reference cut_cross_entropy.py:559-808; AdaptiveCrossEntropyLoss, :1283-1372).
 
 fused_linear_cross_entropy* / FusedLinearCrossEntropy* (reference
 triton_kernels.py:2308-2817), triton_fused_linear_cross_entropy* /
@@ -190,3 +192,84 @@ def test_legacy_chunked_cross_entropy():
     torch.cuda.synchronize()
     assert_loss_close(float(loss.detach()), float(rl), "loss")
     assert_grad_close(xd.grad.float().cpu().numpy().reshape(rg.shape), rg, "dlogits")
+
+
+def test_forward_and_backward_static_methods():
+    from chronicals_amd.kernels.cut_cross_entropy import CutCrossEntropyBackward, CutCrossEntropyForward
+    h, w, lab, b = _case(300, 96, 4001, seed=9, bias=True, oob=True)
+    hd, wd, bd = _dev(h, w, b)
+    loss, lse, tgt, valid = CutCrossEntropyForward.forward(hd, wd, lab.to(DEV), bd, 1024, IGNORE, 0.1, 1e-3)
+    rl, rlse, rt, rvalid = oracle.forward(bf16_exact(h).numpy(), bf16_exact(w).numpy(), lab.numpy(), b.numpy(),
+                                          label_smoothing=0.1, z_loss_weight=1e-3)
+    torch.cuda.synchronize()
+    assert_loss_close(float(loss), float(rl), "loss")
+    np.testing.assert_allclose(lse.cpu().numpy(), rlse, rtol=2e-5, atol=2e-5)
+    np.testing.assert_allclose(tgt.cpu().numpy(), rt, rtol=1e-4, atol=2e-4)
+    assert np.array_equal(valid.cpu().numpy(), rvalid)
+    # scalar grad_output: the mean loss's gradients times it
+    gh_, gw_, gb_ = CutCrossEntropyBackward.backward(hd, wd, lab.to(DEV), lse, valid, torch.tensor(2.0, device=DEV),
+                                                     bd, 1024, IGNORE, 0.1, 1e-3)
+    _, _, gh, gw, gb = _oracle(h, w, lab, b, 0.1, 1e-3, "mean", "logv", grad_output=np.array([2.0]))
+    torch.cuda.synchronize()
+    assert gh_.dtype == hd.dtype and gw_.dtype == wd.dtype and gb_.dtype == bd.dtype
+    assert_grad_close(gh_.float().cpu().numpy(), gh, "dH")
+    assert_grad_close(gw_.float().cpu().numpy(), gw, "dW")
+    assert_grad_close(gb_.float().cpu().numpy(), gb, "dB")
+    # a narrower valid mask than the labels', and a per-row grad_output (row n scaled by g[n] / n_valid)
+    vm = valid.clone()
+    vm[::3] = False
+    go = torch.rand(300, generator=torch.Generator().manual_seed(10))
+    gh_, gw_, _ = CutCrossEntropyBackward.backward(hd, wd, lab.to(DEV), lse, vm, go.to(DEV), None, 1024, IGNORE,
+                                                   0.1, 1e-3)
+    lab2 = lab.clone()
+    lab2[~vm.cpu()] = IGNORE
+    nv = int(vm.sum())
+    _, _, gh, gw, _ = oracle.loss_and_grads(bf16_exact(h).numpy(), bf16_exact(w).numpy(), lab2.numpy(), None,
+                                            label_smoothing=0.1, z_loss_weight=1e-3, reduction="none",
+                                            grad_output=go.numpy() / nv)
+    torch.cuda.synchronize()
+    assert_grad_close(gh_.float().cpu().numpy(), gh, "dH per-row")
+    assert_grad_close(gw_.float().cpu().numpy(), gw, "dW per-row")
+
+
+@pytest.mark.parametrize("V", [5003, 40000])
+@pytest.mark.parametrize("mode", ["hidden", "logits"])
+def test_adaptive_cross_entropy_loss(V, mode):
+    import torch.nn.functional as F
+    from chronicals_amd.kernels.cut_cross_entropy import AdaptiveCrossEntropyLoss
+    eps, z = 0.1, 1e-3
+    h, w, lab, _ = _case(200, 64, V, seed=11)
+    loss_fn = AdaptiveCrossEntropyLoss(label_smoothing=eps, z_loss_weight=z)
+    small = V < loss_fn.small_vocab_threshold
+    print(f"adaptive V={V} mode={mode} small={small}", flush=True)
+    if mode == "hidden":
+        hd, wd, _ = _dev(h, w, None)
+        loss = loss_fn(hd, wd, lab.to(DEV))
+        loss.backward()
+        if small:
+            # torch's CrossEntropyLoss over the logits (uniform smoothing, no z-loss)
+            rl, _, gh, gw, _ = _oracle(h, w, lab, None, eps, 0.0, "mean", "uniform")
+        else:
+            rl, _, gh, gw, _ = _oracle(h, w, lab, None, eps, z, "mean", "logv")
+        dh, dw, _ = _grads(hd, wd, None)
+        assert_loss_close(float(loss.detach()), float(rl), "loss")
+        assert_grad_close(dh, gh, "dH")
+        assert_grad_close(dw, gw, "dW")
+    else:
+        x = (bf16_exact(h) @ bf16_exact(w).t()).to(torch.bfloat16)
+        xd = x.to(DEV).requires_grad_(True)
+        loss = loss_fn(xd, lab.to(DEV))
+        loss.backward()
+        xr = x.double().requires_grad_(True)
+        if small:
+            ref = F.cross_entropy(xr, lab, ignore_index=IGNORE, label_smoothing=eps)
+        else:
+            valid = lab != IGNORE
+            lse_r = torch.logsumexp(xr, -1)
+            t = xr.gather(1, torch.where(valid, lab, 0)[:, None])[:, 0]
+            rows = ((1 - eps) * (lse_r - t) + eps * np.log(V) + z * lse_r ** 2) * valid
+            ref = rows.sum() / valid.sum()
+        (rg,) = torch.autograd.grad(ref, xr)
+        torch.cuda.synchronize()
+        assert_loss_close(float(loss.detach()), float(ref), "loss")
+        assert_grad_close(xd.grad.float().cpu().numpy(), rg.numpy(), "dlogits")

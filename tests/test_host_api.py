@@ -103,7 +103,8 @@ def test_custom_op_fake_shapes_forward(reduction, loss_shape):
         h = torch.empty(300, 128, dtype=torch.bfloat16, device="cuda")
         w = torch.empty(1000, 128, dtype=torch.bfloat16, device="cuda")
         lab = torch.empty(300, dtype=torch.int64, device="cuda")
-        loss, lse, nv = torch.ops.chronicals_hip.cce_fwd(h, w, lab, None, -100, 0.0, 0.0, 0, reduction)
+        loss, lse, nv, tgt = torch.ops.chronicals_hip.cce_fwd(h, w, lab, None, -100, 0.0, 0.0, 0, reduction)
+        assert tuple(tgt.shape) == (300,) and tgt.dtype == torch.float32
         assert tuple(loss.shape) == loss_shape and loss.dtype == torch.float32
         assert tuple(lse.shape) == (300,) and lse.dtype == torch.float32
         assert tuple(nv.shape) == (1,) and nv.dtype == torch.int32
@@ -246,3 +247,25 @@ def test_fused_linear_apis_refuse_cpu_tensors():
                  lambda: fl.chunked_cross_entropy(torch.randn(1, 4, 10), lab.view(1, 4))):
         with pytest.raises(RuntimeError, match="HIP devices"):
             call()
+
+
+def test_reference_module_public_names_all_present():
+    # every public name of chronicals/kernels/cut_cross_entropy.py (:47-1430)
+    for name in ("CHUNK_SIZE_SMALL_VOCAB", "CHUNK_SIZE_MEDIUM_VOCAB", "CHUNK_SIZE_LARGE_VOCAB",
+                 "DEFAULT_VOCAB_CHUNK_SIZE", "TRITON_BLOCK_SIZE", "TRITON_BLOCK_SIZE_MAX", "get_optimal_chunk_size",
+                 "CutCrossEntropyForward", "CutCrossEntropyBackward", "CutCrossEntropyFunction", "cut_cross_entropy",
+                 "CutCrossEntropyLoss", "chunked_cross_entropy_loss", "ChunkedCrossEntropyLoss",
+                 "AdaptiveCrossEntropyLoss", "compute_z_loss", "estimate_memory_savings"):
+        assert hasattr(cce, name), name
+    sig = lambda f: list(inspect.signature(f).parameters)  # noqa: E731
+    assert sig(cce.CutCrossEntropyForward.forward) == ["hidden", "weight", "labels", "bias", "chunk_size",
+                                                       "ignore_index", "label_smoothing", "z_loss_weight",
+                                                       "use_kahan"]
+    assert sig(cce.CutCrossEntropyBackward.backward) == ["hidden", "weight", "labels", "logsumexp", "valid_mask",
+                                                         "grad_output", "bias", "chunk_size", "ignore_index",
+                                                         "label_smoothing", "z_loss_weight"]
+    a = cce.AdaptiveCrossEntropyLoss()
+    assert (a.small_vocab_threshold, a.large_vocab_threshold, a.ignore_index, a.label_smoothing,
+            a.z_loss_weight) == (32000, 100000, -100, 0.0, 0.0)
+    with pytest.raises(RuntimeError, match="HIP devices"):
+        a(torch.randn(4, 8), torch.randn(40000, 8), torch.zeros(4, dtype=torch.long))
