@@ -164,6 +164,8 @@ def main() -> int:
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (PMC calibration) and exit")
+    ap.add_argument("--frozen-weight", action="store_true",
+                    help="lm_head weight frozen (LoRA): the step computes dHidden only, 4*N*V*d credited FLOPs")
     ap.add_argument("--blas-reference", action="store_true",
                     help="only time torch.matmul (hipBLASLt) on the path's GEMM shapes and exit")
     ap.add_argument("--workload", choices=("fused", "logits"), default="fused",
@@ -196,8 +198,9 @@ def main() -> int:
     torch.cuda.set_device(dev)
     h, w, lab = make_inputs(cfg, seed=0, device=dev, gen_device="cuda")
     h = h.to(torch.bfloat16).requires_grad_(True)
-    w = w.to(torch.bfloat16).requires_grad_(True)
+    w = w.to(torch.bfloat16).requires_grad_(not args.frozen_weight)
     N, d, V = cfg.N, cfg.d, cfg.V
+    credited_step = (4.0 if args.frozen_weight else 6.0) * N * V * d
 
     def step():
         h.grad = None
@@ -256,13 +259,13 @@ def main() -> int:
     try:
         with open(TRAFFIC_FILE) as f:
             tr = json.load(f)
-        if tr.get("config") == cfg.name and tr.get("kernel") == dom:
+        if tr.get("config") == cfg.name and tr.get("kernel") == dom and not args.frozen_weight:
             traffic = tr.get("hbm_bytes_per_launch")
             clock = tr.get("mfma_busy_and_clock", {}).get(dom, {}).get("clock_ghz")
     except (OSError, ValueError):
         pass
 
-    step_tflops = 6.0 * N * V * d / (ms * 1e-3) / 1e12
+    step_tflops = credited_step / (ms * 1e-3) / 1e12
     out = {
         "metric": "fused linear-CE fwd+bwd tokens/s and % bf16 MFMA peak, N=16k V=152k",
         "value": N / (ms * 1e-3),
@@ -278,8 +281,9 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) hidden, N(0,0.02) W, uniform labels, 5% ignore_index)",
         "config": {"workload": f"{cfg.name}: fused linear-CE fwd+bwd N={N} d={d} V={V} bf16, "
-                               f"{int(cfg.ignore_frac * 100)}% ignore_index, {cfg.reduction}; grads dHidden, dW",
-                   "N": N, "d": d, "V": V, "chunk_size": args.chunk},
+                               f"{int(cfg.ignore_frac * 100)}% ignore_index, {cfg.reduction}; grads "
+                               + ("dHidden only (frozen lm_head weight)" if args.frozen_weight else "dHidden, dW"),
+                   "N": N, "d": d, "V": V, "chunk_size": args.chunk, "frozen_weight": bool(args.frozen_weight)},
         "pct_bf16_peak": 100.0 * step_tflops / PEAK_BF16_TFLOPS,
         "step_tflops_algorithmic": step_tflops,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
