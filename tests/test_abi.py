@@ -191,3 +191,15 @@ def test_built_kernels_do_not_spill():
     for name, r in kernels.items():
         assert int(r.get("VGPRs_Spill", 0)) == 0, f"{name} spills {r['VGPRs_Spill']} VGPRs"
         assert int(r.get("LDS_Size_[bytes/block]", 0)) <= 160 * 1024, name
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    # no fallback: without the built HIP library the package raises instead of computing elsewhere
+    import subprocess
+    import sys
+    code = ("from chronicals_amd import _lib\n"
+            "try:\n    _lib.load()\nexcept ImportError as e:\n    print('IMPORT_ERROR', e)\n")
+    env = dict(os.environ, CHRONICALS_CCE_LIB=str(tmp_path / "absent.so"))
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, cwd=REPO,
+                         timeout=300)
+    assert "IMPORT_ERROR" in out.stdout and "not found" in out.stdout, out.stdout + out.stderr
