@@ -85,7 +85,8 @@ def _rows(logits: torch.Tensor, labels: torch.Tensor, what: str) -> Tuple[torch.
         raise RuntimeError(f"logits must be [..., V], got shape {tuple(logits.shape)}")
     V = logits.shape[-1]
     x = logits.reshape(-1, V)
-    if x.shape[0] > 1 and x.stride(-1) != 1:
+    # the kernels take unit-stride rows that do not overlap (row stride >= V)
+    if (V > 1 and x.stride(-1) != 1) or (x.shape[0] > 1 and x.stride(0) < V):
         x = x.contiguous()
     if x.dtype not in (torch.bfloat16, torch.float16, torch.float32):
         x = x.float()

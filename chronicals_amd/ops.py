@@ -168,7 +168,7 @@ _LOGITS_DTYPES = {torch.bfloat16: _lib.CCE_DTYPE_BF16, torch.float16: _lib.CCE_D
 def _check_logits(logits: Tensor, labels: Tensor) -> None:
     if logits.dtype not in _LOGITS_DTYPES:
         raise RuntimeError(f"logits dtype {logits.dtype} not supported (bf16, fp16, fp32)")
-    if logits.dim() != 2 or logits.stride(1) != 1:
+    if logits.dim() != 2 or (logits.shape[1] > 1 and logits.stride(1) != 1):
         raise RuntimeError(f"ce_logits ops take [N, V] logits with a contiguous last dimension, got "
                            f"shape {tuple(logits.shape)} strides {logits.stride()}")
     if labels.dim() != 1 or labels.shape[0] != logits.shape[0] or labels.dtype not in (torch.int64, torch.int32):

@@ -289,3 +289,18 @@ def test_torch_compile_fullgraph():
     torch.cuda.synchronize()
     assert torch.allclose(l1, l2, rtol=1e-6)
     assert torch.equal(x1.grad, x2.grad)
+
+
+def test_overlapping_and_single_row_views_are_copied():
+    m = _mod()
+    row = torch.randn(1, 4099).to(DEV, torch.bfloat16)
+    lab = torch.tensor([7, 4000, 12], device=DEV)
+    x = row.expand(3, 4099)  # row stride 0
+    loss = m.chunked_cross_entropy_loss(x, lab)
+    ref = torch.nn.functional.cross_entropy(row.float().expand(3, 4099), lab)
+    assert_loss_close(float(loss), float(ref), "expanded rows")
+    t = torch.randn(4099, 2).to(DEV, torch.bfloat16)
+    xt = t[:, :1].t()  # one row, last-dimension stride 2
+    l1 = m.chunked_cross_entropy_loss(xt, lab[:1])
+    r1 = torch.nn.functional.cross_entropy(xt.float(), lab[:1])
+    assert_loss_close(float(l1), float(r1), "strided single row")
