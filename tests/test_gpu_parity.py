@@ -270,3 +270,52 @@ def test_torch_compile_fullgraph_matches_eager(gpu):
     compiled = run(torch.compile(loss_fn, backend="aot_eager", fullgraph=True))
     for a, c, name in zip(eager, compiled, ("loss", "dh", "dw", "db")):
         assert torch.equal(a, c), name
+
+
+def test_peak_memory_below_materialised_logits(gpu):
+    """The reference's memory test (tests/test_lora_optimizations.py:297-342): fwd+bwd peak memory of the
+    fused loss below 0.8x that of materialised logits + F.cross_entropy, at its shape N=1024, d=256, V=32000."""
+    import torch.nn.functional as F
+    from chronicals_amd.kernels.cut_cross_entropy import cut_cross_entropy
+    g = torch.Generator().manual_seed(3)
+    h = torch.randn(1024, 256, generator=g).to(gpu, torch.bfloat16).requires_grad_(True)
+    w = (torch.randn(32000, 256, generator=g) * 0.02).to(gpu, torch.bfloat16).requires_grad_(True)
+    lab = torch.randint(0, 32000, (1024,), generator=g).to(gpu)
+
+    def peak(fn):
+        h.grad = None
+        w.grad = None
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        fn().backward()
+        torch.cuda.synchronize()
+        return torch.cuda.max_memory_allocated() - base
+
+    p_cce = peak(lambda: cut_cross_entropy(h, w, lab))
+    p_mat = peak(lambda: F.cross_entropy((h @ w.t()).float(), lab))
+    assert p_cce < 0.8 * p_mat, (p_cce, p_mat)
+
+
+def test_peak_memory_bounded_by_chunk_at_C2(gpu):
+    """At C2 the fwd+bwd holds O(N*chunk + N*d) extra memory, never the N x V logits."""
+    from chronicals_amd import _lib
+    from chronicals_amd.kernels.cut_cross_entropy import cut_cross_entropy
+    N, d, V, chunk = 16384, 896, 151936, 8192
+    g = torch.Generator(device=gpu).manual_seed(0)
+    h = torch.randn(N, d, generator=g, device=gpu).to(torch.bfloat16).requires_grad_(True)
+    w = (torch.randn(V, d, generator=g, device=gpu) * 0.02).to(torch.bfloat16).requires_grad_(True)
+    lab = torch.randint(0, V, (N,), generator=g, device=gpu)
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    cut_cross_entropy(h, w, lab, chunk_size=chunk).backward()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated() - base
+    grads = N * d * 2 + V * d * 2
+    bound = (grads + _lib.backward_workspace_bytes(N, d, V, chunk, True, True)
+             + _lib.forward_workspace_bytes(N, d, V, _lib.CCE_REDUCTION_MEAN) + 64 * 2 ** 20)
+    print(f"C2 peak extra {peak / 2**20:.0f} MiB, bound {bound / 2**20:.0f} MiB, "
+          f"materialised fp32 logits + grad {N * V * 8 / 2**20:.0f} MiB", flush=True)
+    assert peak <= bound
+    assert peak < 0.1 * N * V * 8
