@@ -168,8 +168,10 @@ def main() -> int:
                     help="lm_head weight frozen (LoRA): the step computes dHidden only, 4*N*V*d credited FLOPs")
     ap.add_argument("--blas-reference", action="store_true",
                     help="only time torch.matmul (hipBLASLt) on the path's GEMM shapes and exit")
-    ap.add_argument("--workload", choices=("fused", "logits"), default="fused",
-                    help="fused: linear-CE from hidden + lm_head (default); logits: CE over existing logits")
+    ap.add_argument("--workload", choices=("fused", "logits", "logits-fused"), default="fused",
+                    help="fused: linear-CE from hidden + lm_head (default); logits: CE over existing logits, "
+                         "forward + autograd backward; logits-fused: loss and gradient in one kernel "
+                         "(liger_cross_entropy_forward with compute_grads)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -180,7 +182,7 @@ def main() -> int:
         copy_calibration(args.copy_calibration)
         return 0
 
-    if args.workload == "logits":
+    if args.workload in ("logits", "logits-fused"):
         return bench_logits(args)
     if args.blas_reference:
         from tests.cce_common import CONFIGS
@@ -311,8 +313,10 @@ def bench_logits(args) -> int:
     import torch
 
     from chronicals_amd import _lib
-    from chronicals_amd.kernels.logits_cross_entropy import chunked_cross_entropy_loss
+    from chronicals_amd.kernels.logits_cross_entropy import chunked_cross_entropy_loss, liger_cross_entropy_forward
     from tests.cce_common import CONFIGS
+
+    fused = args.workload == "logits-fused"
 
     cfg = CONFIGS[args.config]
     N, V = cfg.N, cfg.V
@@ -324,10 +328,15 @@ def bench_logits(args) -> int:
     lab[torch.rand(N, generator=g, device=dev) < cfg.ignore_frac] = -100
 
     def step():
+        if fused:
+            # the gradient overwrites the logits, as the reference's kernel does; later steps run on those values
+            return liger_cross_entropy_forward(xf, lab, compute_grads=True)[0]
         x.grad = None
         loss = chunked_cross_entropy_loss(x, lab)
         loss.backward()
         return loss
+
+    xf = x.detach() if fused else None
 
     for _ in range(args.warmup):
         step()
@@ -350,7 +359,7 @@ def bench_logits(args) -> int:
         return step_ms[min(len(step_ms) - 1, int(round(q * (len(step_ms) - 1))))]
 
     kernels = {}
-    for k in (_lib.CCE_KERNEL_LOGITS_FWD, _lib.CCE_KERNEL_LOGITS_BWD):
+    for k in (_lib.CCE_KERNEL_LOGITS_FWD, _lib.CCE_KERNEL_LOGITS_BWD, _lib.CCE_KERNEL_LOGITS_FUSED):
         tot_ms, n, by, _ = _lib.kernel_timing_read(k)
         if n == 0:
             continue
@@ -363,7 +372,7 @@ def bench_logits(args) -> int:
         }
     dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
     kd = kernels[dom]
-    step_bytes = 3.0 * N * V * 2
+    step_bytes = (2.0 if fused else 3.0) * N * V * 2
     traffic = None
     try:
         with open(TRAFFIC_LOGITS_FILE) as f:
@@ -373,7 +382,8 @@ def bench_logits(args) -> int:
     except (OSError, ValueError):
         pass
     out = {
-        "metric": "logits-in CE fwd+bwd tokens/s and % HBM peak, N=16k V=152k bf16 logits",
+        "metric": ("logits-in CE loss+gradient (one kernel) tokens/s and % HBM peak, N=16k V=152k bf16 logits"
+                   if fused else "logits-in CE fwd+bwd tokens/s and % HBM peak, N=16k V=152k bf16 logits"),
         "value": N / (ms * 1e-3),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -386,8 +396,11 @@ def bench_logits(args) -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,9) bf16 logits, uniform labels, 5% ignore_index)",
-        "config": {"workload": f"logits-in CE (chunked_cross_entropy_loss) fwd+bwd over [{N}, {V}] bf16 logits, "
-                               f"mean; grad dlogits bf16", "N": N, "V": V},
+        "config": {"workload": (f"logits-in CE loss + gradient in one kernel (liger_cross_entropy_forward, "
+                                f"compute_grads) over [{N}, {V}] bf16 logits, mean; gradient bf16 over the logits"
+                                if fused else
+                                f"logits-in CE (chunked_cross_entropy_loss) fwd+bwd over [{N}, {V}] bf16 logits, "
+                                f"mean; grad dlogits bf16"), "N": N, "V": V},
         "step_gbs_algorithmic": step_bytes / (ms * 1e-3) / 1e9,
         "roofline": {"bound": "hbm", "achieved": kd["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": kd["gbs"] / PEAK_HBM_GBS, "traffic": traffic,

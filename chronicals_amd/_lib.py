@@ -33,10 +33,12 @@ CCE_KERNEL_BWD_DHDW = 4
 CCE_KERNEL_BWD_BAND = 5
 CCE_KERNEL_LOGITS_FWD = 6
 CCE_KERNEL_LOGITS_BWD = 7
-CCE_KERNEL_KINDS = 8
+CCE_KERNEL_LOGITS_FUSED = 8
+CCE_KERNEL_KINDS = 9
 KERNEL_KIND_NAMES = {CCE_KERNEL_FWD_LSE: "fwd_lse", CCE_KERNEL_BWD_GRAD: "bwd_grad", CCE_KERNEL_BWD_DH: "bwd_dh",
                      CCE_KERNEL_BWD_DW: "bwd_dw", CCE_KERNEL_BWD_DHDW: "bwd_dhdw", CCE_KERNEL_BWD_BAND: "bwd_band",
-                     CCE_KERNEL_LOGITS_FWD: "logits_fwd", CCE_KERNEL_LOGITS_BWD: "logits_bwd"}
+                     CCE_KERNEL_LOGITS_FWD: "logits_fwd", CCE_KERNEL_LOGITS_BWD: "logits_bwd",
+                     CCE_KERNEL_LOGITS_FUSED: "logits_fused"}
 
 REDUCTIONS = {"none": CCE_REDUCTION_NONE, "mean": CCE_REDUCTION_MEAN, "sum": CCE_REDUCTION_SUM}
 
@@ -80,6 +82,14 @@ SIGNATURES = {
         _vp, _vp, _i64, _i64, _i64,          # lse, n_valid, N, V, ignore_index
         _f32, _f32, _i32, _i32,              # label_smoothing, z_loss_weight, smoothing_form, reduction
         _vp, _i32, _i64, _vp,                # grad_logits, grad_dtype, ld_grad, stream
+    ]),
+    "cce_logits_forward_backward": (_i32, [
+        _vp, _i32, _i64, _vp, _i32,          # logits, dtype, ld, labels, labels_int64
+        _i64, _i64, _i64,                    # N, V, ignore_index
+        _f32, _f32, _i32, _i32, _i32,        # label_smoothing, z_loss_weight, smoothing_form, reduction, grad_mean
+        _vp, _vp, _vp,                       # loss_out, lse_out, n_valid_out
+        _vp, _i32, _i64,                     # grad_logits, grad_dtype, ld_grad
+        _vp, _sz, _vp,                       # workspace, workspace_bytes, stream
     ]),
     "cce_kernel_timing_enable": (_i32, [_i32]),
     "cce_kernel_timing_read": (_i32, [_i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64),

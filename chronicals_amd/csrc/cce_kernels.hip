@@ -1293,24 +1293,35 @@ struct RowSplit {
   }
 };
 
-// Calls f(c, chunk) for this thread's 16-byte chunks c = tid, tid + 256, ...
+// Calls f(c, chunk) for this thread's 16-byte chunks c = tid, tid + NT, ...
 // below `chunks`, issuing four loads before the first use so that every wave
-// keeps 4 KB of HBM reads in flight.
-template <typename F>
+// keeps 4 KB of HBM reads in flight.  kStream: non-temporal loads (data read
+// once); otherwise ordinary loads, which leave the lines in the caches for a
+// second read.
+template <int NT = 256, bool kStream = true>
+__device__ __forceinline__ u32x4 chunk_load(const u32x4* p) {
+  if constexpr (kStream)
+    return __builtin_nontemporal_load(p);
+  else
+    return *p;
+}
+template <int NT = 256, bool kStream = true, typename F>
 __device__ __forceinline__ void for_each_chunk(const u32x4* __restrict__ body, int chunks, int tid, F&& f) {
   constexpr int U = 4;
   int c = tid;
-  for (; c + (U - 1) * 256 < chunks; c += U * 256) {
+  for (; c + (U - 1) * NT < chunks; c += U * NT) {
     u32x4 raw[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) raw[u] = __builtin_nontemporal_load(body + c + u * 256);
+    for (int u = 0; u < U; ++u) raw[u] = chunk_load<NT, kStream>(body + c + u * NT);
 #pragma unroll
-    for (int u = 0; u < U; ++u) f(c + u * 256, raw[u]);
+    for (int u = 0; u < U; ++u) f(c + u * NT, raw[u]);
   }
-  for (; c < chunks; c += 256) f(c, __builtin_nontemporal_load(body + c));
+  for (; c < chunks; c += NT) f(c, chunk_load<NT, kStream>(body + c));
 }
 
-// Workgroup-wide merge of base-2 (max, sum) pairs; every thread gets the result.
+// Workgroup-wide merge of base-2 (max, sum) pairs over NW waves; every thread
+// gets the result.  red holds 2*NW floats.
+template <int NW = 4>
 __device__ inline void block_merge_ms(float& m, float& s, float* red) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
@@ -1328,7 +1339,7 @@ __device__ inline void block_merge_ms(float& m, float& s, float* red) {
   m = red[0];
   s = red[1];
 #pragma unroll
-  for (int k = 1; k < 4; ++k) {
+  for (int k = 1; k < NW; ++k) {
     const float m2 = red[2 * k], s2 = red[2 * k + 1];
     const float mn = fmaxf(m, m2);
     s = s * fast_exp2(m - mn) + s2 * fast_exp2(m2 - mn);
@@ -1336,14 +1347,18 @@ __device__ inline void block_merge_ms(float& m, float& s, float* red) {
   }
 }
 
-// Workgroup-wide sum; every thread gets the result.
+// Workgroup-wide sum over NW waves (fixed order); every thread gets the result.
+template <int NW = 4>
 __device__ inline float block_sum(float v, float* red) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
   __syncthreads();  // red may still be read by an earlier merge
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
-  return (red[0] + red[1]) + (red[2] + red[3]);
+  float t = red[0];
+#pragma unroll
+  for (int k = 1; k < NW; ++k) t += red[k];
+  return t;
 }
 
 // Forward: lse[n] = log sum exp(x), the row loss (0 for rows labelled
@@ -1470,6 +1485,123 @@ __global__ __launch_bounds__(256) void ce_logits_bwd_kernel(const float* __restr
 #pragma unroll
     for (int k = 0; k < kOut; ++k) __builtin_nontemporal_store(out[k], dbody + c * kOut + k);
   });
+}
+
+// Number of rows whose label is not ignore_index (one workgroup, fixed order).
+__global__ __launch_bounds__(1024) void count_valid_kernel(const void* labels, int labels64, int N, long ignore_index,
+                                                           int32_t* __restrict__ out) {
+  __shared__ int part[1024];
+  int c = 0;
+  for (int n = threadIdx.x; n < N; n += 1024) c += load_label(labels, labels64, n) != ignore_index;
+  part[threadIdx.x] = c;
+  __syncthreads();
+  for (int o = 512; o >= 1; o >>= 1) {
+    if ((int)threadIdx.x < o) part[threadIdx.x] += part[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[0] = part[0];
+}
+
+// Loss and gradient in one kernel: a workgroup of kFusedThreads takes rows
+// n = blockIdx.x, blockIdx.x + gridDim.x, ...; for each it streams the row
+// once for lse (as ce_logits_fwd_kernel) and again for the gradient (as
+// ce_logits_bwd_kernel with grad_out = 1).  The grid bounds the rows in
+// flight, so the second read of a row finds it in the memory-side cache.
+// g_n = 1/max(n_valid,1) when n_valid is given, else 1.  dX may be X itself:
+// each row's first pass ends at a barrier before its second pass writes.
+constexpr int kFusedThreads = 512;
+constexpr bool kFusedPass2Stream = true;  // the row's last read: non-temporal
+template <typename T, typename TO>
+__global__ __launch_bounds__(kFusedThreads) void ce_logits_fused_kernel(
+    const T* X, long ld, const void* labels, int labels64, int N, int V, long ignore_index, float eps, float zw,
+    float logV, int smooth_mode, const int32_t* __restrict__ n_valid, float* __restrict__ lse_out,
+    float* __restrict__ rowloss, float* __restrict__ bsum, int* __restrict__ bcnt, TO* dX, long ldg) {
+  constexpr int NW = kFusedThreads / 64;
+  constexpr int E = RowSplit<T>::E;
+  constexpr int kOut = sizeof(TO) / sizeof(T);
+  static_assert(kOut * sizeof(T) == sizeof(TO), "output element size must be a multiple of the input's");
+  __shared__ float red[2 * NW];
+  const int tid = threadIdx.x;
+  const float g = n_valid ? 1.f / (float)(n_valid[0] > 1 ? n_valid[0] : 1) : 1.f;
+  const bool uni = smooth_mode == CCE_SMOOTH_UNIFORM;
+  for (int n = blockIdx.x; n < N; n += gridDim.x) {
+    const T* row = X + (long)n * ld;
+    TO* drow = dX + (long)n * ldg;
+    const RowSplit<T> sp(row, V);
+    const long lab = load_label(labels, labels64, n);
+    const bool valid = lab != ignore_index;
+    const long t = (valid && lab >= 0 && lab < V) ? lab : -1;
+    float tval = 0.f;
+    if (tid == 0 && t >= 0) tval = elem_to_f32(row[t]);
+    // pass 1: online max / sum-exp (base 2) and the row sum
+    float m = kNegBig, s = 0.f, sx = 0.f;
+    auto add1 = [&](float x) {
+      const float x2 = x * kLog2e, mn = fmaxf(m, x2);
+      s = s * fast_exp2(m - mn) + fast_exp2(x2 - mn);
+      m = mn;
+      sx += x;
+    };
+    if (tid < sp.head) add1(elem_to_f32(row[tid]));
+    if (tid < V - sp.tail_start) add1(elem_to_f32(row[sp.tail_start + tid]));
+    const u32x4* body = reinterpret_cast<const u32x4*>(row + sp.head);
+    // ordinary loads: the lines stay in the memory-side cache for pass 2
+    for_each_chunk<kFusedThreads, false>(body, sp.chunks, tid, [&](int, const u32x4& raw) {
+      const T* v = reinterpret_cast<const T*>(&raw);
+      float x[E], mx = kNegBig, cs = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float xe = elem_to_f32(v[e]);
+        cs += xe;
+        x[e] = xe * kLog2e;
+        mx = fmaxf(mx, x[e]);
+      }
+      const float mn = fmaxf(m, mx);
+      float acc = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc += fast_exp2(x[e] - mn);
+      s = s * fast_exp2(m - mn) + acc;
+      m = mn;
+      sx += cs;
+    });
+    block_merge_ms<NW>(m, s, red);
+    if (uni) sx = block_sum<NW>(sx, red);
+    const float lse = m * kLn2 + logf(s + 1e-10f);
+    if (tid == 0) {
+      const float smooth = uni ? lse - sx / (float)V : logV;
+      const float loss = valid ? (1.f - eps) * (lse - tval) + eps * smooth + zw * lse * lse : 0.f;
+      lse_out[n] = lse;
+      rowloss[n] = loss;
+      bsum[n] = loss;
+      bcnt[n] = valid ? 1 : 0;
+    }
+    // pass 2: the gradient
+    const float cP = valid ? g * ((uni ? 1.f : 1.f - eps) + 2.f * zw * lse) : 0.f;
+    const float cU = valid && uni ? g * eps / (float)V : 0.f;
+    const float cT = valid ? g * (1.f - eps) : 0.f;
+    const float l2 = lse * kLog2e;
+    auto grad1 = [&](int v, float x) { return (cP * fast_exp2(x * kLog2e - l2) - cU) - (v == t ? cT : 0.f); };
+    if ((reinterpret_cast<uintptr_t>(drow + sp.head) & 15u) != 0) {
+      for (int v = tid; v < V; v += kFusedThreads) drow[v] = f32_to_elem<TO>(grad1(v, elem_to_f32(row[v])));
+    } else {
+      if (tid < sp.head) drow[tid] = f32_to_elem<TO>(grad1(tid, elem_to_f32(row[tid])));
+      if (tid < V - sp.tail_start) {
+        const int v = sp.tail_start + tid;
+        drow[v] = f32_to_elem<TO>(grad1(v, elem_to_f32(row[v])));
+      }
+      u32x4* dbody = reinterpret_cast<u32x4*>(drow + sp.head);
+      for_each_chunk<kFusedThreads, kFusedPass2Stream>(body, sp.chunks, tid, [&](int c, const u32x4& raw) {
+        const T* v = reinterpret_cast<const T*>(&raw);
+        u32x4 out[kOut];
+        TO* o = reinterpret_cast<TO*>(out);
+        const int v0 = sp.head + c * E;
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[e] = f32_to_elem<TO>(grad1(v0 + e, elem_to_f32(v[e])));
+#pragma unroll
+        for (int k = 0; k < kOut; ++k) __builtin_nontemporal_store(out[k], dbody + c * kOut + k);
+      });
+    }
+    __syncthreads();  // red is rewritten by the next row's merge
+  }
 }
 
 // Per-row backward coefficients.
@@ -2308,6 +2440,77 @@ int cce_logits_backward(const float* grad_out, const void* logits, int logits_dt
     timing_end(CCE_KERNEL_LOGITS_BWD, st, e0, e1, bytes, bytes);
   }
   HIP_TRY(le);
+  return CCE_OK;
+}
+
+int cce_logits_forward_backward(const void* logits, int logits_dtype, int64_t ld, const void* labels,
+                                int labels_int64, int64_t N, int64_t V, int64_t ignore_index, float label_smoothing,
+                                float z_loss_weight, int smoothing_form, int reduction, int grad_mean, float* loss_out,
+                                float* lse_out, int32_t* n_valid_out, void* grad_logits, int grad_dtype,
+                                int64_t ld_grad, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = check_logits_args(N, V, logits_dtype, ld, reduction, label_smoothing, smoothing_form);
+  if (rc) return rc;
+  if (grad_dtype != logits_dtype && grad_dtype != CCE_DTYPE_F32)
+    return fail(CCE_ERR_INVALID_ARG, "grad_dtype must be the logits' dtype or CCE_DTYPE_F32, got %d", grad_dtype);
+  if (ld_grad < V) return fail(CCE_ERR_INVALID_ARG, "gradient row stride %ld is smaller than V = %ld", (long)ld_grad, (long)V);
+  if (!n_valid_out || (!loss_out && (N > 0 || reduction != CCE_REDUCTION_NONE)) ||
+      (N > 0 && (!logits || !labels || !lse_out || !grad_logits)))
+    return fail(CCE_ERR_INVALID_ARG, "logits, labels, loss_out, lse_out, n_valid_out and grad_logits must not be null");
+  const LogitsLayout need = logits_layout(nullptr, N);
+  if (workspace_bytes < need.bytes || !workspace)
+    return fail(CCE_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need.bytes, workspace_bytes);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const LogitsLayout L = logits_layout(workspace, N);
+  float* rowloss = reduction == CCE_REDUCTION_NONE ? loss_out : L.rowloss;
+  if (N > 0) {
+    if (grad_mean) {
+      hipLaunchKernelGGL(count_valid_kernel, dim3(1), dim3(1024), 0, st, labels, labels_int64, (int)N,
+                         (long)ignore_index, n_valid_out);
+      HIP_TRY(hipGetLastError());
+    }
+    int dev = 0, cus = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    // two rows in flight per CU: their first reads are still in the memory-side
+    // cache when the second pass re-reads them
+    const long rows = (long)(cus > 0 ? cus : 256) * 2;
+    const unsigned grid = (unsigned)(N < rows ? N : rows);
+    const float logV = logf((float)V);
+    const int32_t* nv = grad_mean ? n_valid_out : nullptr;
+    hipEvent_t e0, e1;
+    const bool timed = timing_begin(st, &e0, &e1);
+#define CCE_LAUNCH_LFUSED(T, TO)                                                                                      \
+  hipLaunchKernelGGL((ce_logits_fused_kernel<T, TO>), dim3(grid), dim3(kFusedThreads), 0, st,                        \
+                     static_cast<const T*>(logits), (long)ld, labels, labels_int64, (int)N, (int)V,                  \
+                     (long)ignore_index, label_smoothing, z_loss_weight, logV, smoothing_form, nv, lse_out, rowloss, \
+                     L.bsum, L.bcnt, static_cast<TO*>(grad_logits), (long)ld_grad)
+    const bool f32_out = grad_dtype == CCE_DTYPE_F32;
+    if (logits_dtype == CCE_DTYPE_BF16) {
+      if (f32_out)
+        CCE_LAUNCH_LFUSED(uint16_t, float);
+      else
+        CCE_LAUNCH_LFUSED(uint16_t, uint16_t);
+    } else if (logits_dtype == CCE_DTYPE_F16) {
+      if (f32_out)
+        CCE_LAUNCH_LFUSED(_Float16, float);
+      else
+        CCE_LAUNCH_LFUSED(_Float16, _Float16);
+    } else {
+      CCE_LAUNCH_LFUSED(float, float);
+    }
+#undef CCE_LAUNCH_LFUSED
+    const hipError_t le = hipGetLastError();
+    if (timed) {
+      const double bytes =
+          (double)N * (double)V * (double)(logits_elem_size(logits_dtype) + logits_elem_size(grad_dtype));
+      timing_end(CCE_KERNEL_LOGITS_FUSED, st, e0, e1, bytes, bytes);
+    }
+    HIP_TRY(le);
+  }
+  hipLaunchKernelGGL(fwd_finalize_kernel, dim3(1), dim3(1024), 0, st, L.bsum, L.bcnt, (int)N, reduction, loss_out,
+                     n_valid_out);
+  HIP_TRY(hipGetLastError());
   return CCE_OK;
 }
 

@@ -1,11 +1,14 @@
 """Cross-entropy over logits that already exist, on MI355X.
 
 The callers that hold a [N, V] logits tensor (a model that returns logits,
-evaluation) use one of three reference entry points, all served here by the
-same two HIP row kernels (``cce_logits_forward`` / ``cce_logits_backward`` in
-include/chronicals_cce.h).  Each streams a row once: the forward reads the
-logits (online max / sum-exp, target gather, row sum), the backward reads them
-again and writes the gradient.
+evaluation) use one of three reference entry points, all served here by HIP
+row kernels (``cce_logits_forward`` / ``cce_logits_backward`` /
+``cce_logits_forward_backward`` in include/chronicals_cce.h).  The forward
+reads the logits once (online max / sum-exp, target gather, row sum); the
+autograd backward reads them again and writes the gradient with grad_output
+folded in.  Where the reference computes the gradient inside its forward
+(``liger_cross_entropy_forward(compute_grads=True)``, ``fused_cross_entropy``)
+one kernel does both, re-reading each row from the memory-side cache.
 
   chunked_cross_entropy_loss, ChunkedCrossEntropyLoss
       reference chronicals/kernels/cut_cross_entropy.py:1169-1277.  Label
@@ -197,15 +200,15 @@ def liger_cross_entropy_forward(
     """
     red = _reduction_code(reduction)
     x, lab = _rows(logits, target, "liger_cross_entropy_forward")
-    loss, lse, n_valid = torch.ops.chronicals_hip.ce_logits_fwd(
-        x, lab, int(ignore_index), float(label_smoothing), float(lse_square_scale), _lib.CCE_SMOOTH_UNIFORM, red)
     if compute_grads:
-        ones = torch.ones((1,), dtype=torch.float32, device=x.device)
-        # 'none' gradients are not divided (triton_kernels.py:2942-2943): the 'sum' form
-        gred = _lib.CCE_REDUCTION_SUM if red == _lib.CCE_REDUCTION_NONE else red
-        torch.ops.chronicals_hip.ce_logits_bwd_(ones, x, lab, lse, n_valid, int(ignore_index),
-                                                float(label_smoothing), float(lse_square_scale),
-                                                _lib.CCE_SMOOTH_UNIFORM, gred)
+        # one kernel: loss and gradient, written over the logits; only 'mean'
+        # gradients are divided by n_valid (triton_kernels.py:2946-2947)
+        loss, _, _ = torch.ops.chronicals_hip.ce_logits_fwd_bwd_(
+            x, lab, int(ignore_index), float(label_smoothing), float(lse_square_scale), _lib.CCE_SMOOTH_UNIFORM, red,
+            red == _lib.CCE_REDUCTION_MEAN)
+    else:
+        loss, _, _ = torch.ops.chronicals_hip.ce_logits_fwd(
+            x, lab, int(ignore_index), float(label_smoothing), float(lse_square_scale), _lib.CCE_SMOOTH_UNIFORM, red)
     return (loss if red == _lib.CCE_REDUCTION_NONE else loss.view(())), x
 
 
@@ -280,13 +283,10 @@ def fused_cross_entropy_triton(
     reference kernel stores it); zero rows for ignored labels.
     """
     x, lab = _rows(logits, labels, "fused_cross_entropy")
-    loss, lse, n_valid = torch.ops.chronicals_hip.ce_logits_fwd(
+    # one kernel, as the reference's: mean loss, unscaled fp32 gradient rows
+    loss, _, _, dx = torch.ops.chronicals_hip.ce_logits_fwd_bwd(
         x, lab, int(ignore_index), float(label_smoothing), float(z_loss_weight), _lib.CCE_SMOOTH_UNIFORM,
-        _lib.CCE_REDUCTION_MEAN)
-    ones = torch.ones((1,), dtype=torch.float32, device=x.device)
-    dx = torch.ops.chronicals_hip.ce_logits_bwd(ones, x, lab, lse, n_valid, int(ignore_index),
-                                                float(label_smoothing), float(z_loss_weight),
-                                                _lib.CCE_SMOOTH_UNIFORM, _lib.CCE_REDUCTION_SUM, True)
+        _lib.CCE_REDUCTION_MEAN, False, True)
     return loss.view(()), dx.view(logits.shape)
 
 

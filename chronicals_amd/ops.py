@@ -35,7 +35,8 @@ from torch import Tensor
 
 from . import _lib
 
-__all__ = ["cce_fwd", "cce_bwd", "ce_logits_fwd", "ce_logits_bwd", "ce_logits_bwd_"]
+__all__ = ["cce_fwd", "cce_bwd", "ce_logits_fwd", "ce_logits_bwd", "ce_logits_bwd_", "ce_logits_fwd_bwd",
+           "ce_logits_fwd_bwd_"]
 
 
 def _stream(device: torch.device) -> int:
@@ -255,3 +256,68 @@ def ce_logits_bwd_(grad_out: Tensor, logits: Tensor, labels: Tensor, lse: Tensor
 def _ce_logits_bwd__fake(grad_out, logits, labels, lse, n_valid, ignore_index, label_smoothing, z_loss_weight,
                          smoothing_form, reduction):
     return None
+
+
+# ---------------------------------------------------------------------------
+# Loss and gradient in one kernel (cce_logits_forward_backward)
+#
+#   chronicals_hip::ce_logits_fwd_bwd(logits, labels, ignore_index, label_smoothing,
+#                                     z_loss_weight, smoothing_form, reduction,
+#                                     grad_mean, f32_grad) -> (loss, lse, n_valid, grad_logits)
+#   chronicals_hip::ce_logits_fwd_bwd_(...without f32_grad...) -> (loss, lse, n_valid),
+#                                     the gradient written over the logits
+# ---------------------------------------------------------------------------
+
+def _logits_forward_backward(logits: Tensor, labels: Tensor, ignore_index: int, label_smoothing: float,
+                             z_loss_weight: float, smoothing_form: int, reduction: int, grad_mean: bool,
+                             out: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+    _check_logits(logits, labels)
+    lib = _lib.load()
+    device = logits.device
+    N, V = logits.shape
+    with torch.cuda.device(device):
+        ws = torch.empty(_lib.logits_forward_workspace_bytes(N, V, reduction), dtype=torch.uint8, device=device)
+        loss = torch.empty((N,) if reduction == _lib.CCE_REDUCTION_NONE else (1,), dtype=torch.float32,
+                           device=device)
+        lse = torch.empty((N,), dtype=torch.float32, device=device)
+        n_valid = torch.empty((1,), dtype=torch.int32, device=device)
+        _lib.check(lib.cce_logits_forward_backward(
+            logits.data_ptr(), _LOGITS_DTYPES[logits.dtype], _row_stride(logits), labels.data_ptr(),
+            int(labels.dtype == torch.int64), N, V, int(ignore_index), float(label_smoothing), float(z_loss_weight),
+            int(smoothing_form), int(reduction), int(bool(grad_mean)), loss.data_ptr(), lse.data_ptr(),
+            n_valid.data_ptr(), out.data_ptr(), _LOGITS_DTYPES[out.dtype], _row_stride(out), ws.data_ptr(),
+            ws.numel(), _stream(device)))
+    return loss, lse, n_valid
+
+
+@torch.library.custom_op("chronicals_hip::ce_logits_fwd_bwd", mutates_args=(), device_types="cuda")
+def ce_logits_fwd_bwd(logits: Tensor, labels: Tensor, ignore_index: int, label_smoothing: float, z_loss_weight: float,
+                      smoothing_form: int, reduction: int, grad_mean: bool,
+                      f32_grad: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    dx = torch.empty(tuple(logits.shape), dtype=torch.float32 if f32_grad else logits.dtype, device=logits.device)
+    loss, lse, n_valid = _logits_forward_backward(logits, labels, ignore_index, label_smoothing, z_loss_weight,
+                                                  smoothing_form, reduction, grad_mean, dx)
+    return loss, lse, n_valid, dx
+
+
+@ce_logits_fwd_bwd.register_fake
+def _ce_logits_fwd_bwd_fake(logits, labels, ignore_index, label_smoothing, z_loss_weight, smoothing_form, reduction,
+                            grad_mean, f32_grad):
+    loss, lse, nv = _ce_logits_fwd_fake(logits, labels, ignore_index, label_smoothing, z_loss_weight, smoothing_form,
+                                        reduction)
+    return loss, lse, nv, logits.new_empty(tuple(logits.shape), dtype=torch.float32 if f32_grad else logits.dtype)
+
+
+@torch.library.custom_op("chronicals_hip::ce_logits_fwd_bwd_", mutates_args=("logits",), device_types="cuda")
+def ce_logits_fwd_bwd_(logits: Tensor, labels: Tensor, ignore_index: int, label_smoothing: float,
+                       z_loss_weight: float, smoothing_form: int, reduction: int,
+                       grad_mean: bool) -> Tuple[Tensor, Tensor, Tensor]:
+    return _logits_forward_backward(logits, labels, ignore_index, label_smoothing, z_loss_weight, smoothing_form,
+                                    reduction, grad_mean, logits)
+
+
+@ce_logits_fwd_bwd_.register_fake
+def _ce_logits_fwd_bwd__fake(logits, labels, ignore_index, label_smoothing, z_loss_weight, smoothing_form, reduction,
+                             grad_mean):
+    return _ce_logits_fwd_fake(logits, labels, ignore_index, label_smoothing, z_loss_weight, smoothing_form,
+                               reduction)

@@ -165,16 +165,35 @@ int cce_logits_backward(const float* grad_out, const void* logits, int logits_dt
                         int reduction, void* grad_logits, int grad_dtype, int64_t ld_grad, void* stream);
 
 /*
+ * Loss and gradient in one kernel, for the callers whose reference computes
+ * both in its forward: fused_cross_entropy_kernel (triton_kernels.py:141-210)
+ * and _liger_ce_kernel with COMPUTE_GRADS (:2839-2958).  Computes what
+ * cce_logits_forward does and, in the same pass over each row, writes the
+ * gradient of cce_logits_backward with grad_out = 1 and g_n =
+ * 1/max(n_valid,1) if grad_mean, else 1 (the reference kernels' 'mean' and
+ * unscaled forms, :2946-2947, :197-206).  Each row is read twice (the second
+ * time mostly from the memory-side cache) and its gradient written once.
+ * grad_logits may be the logits buffer itself (same dtype and stride).
+ * Workspace from cce_logits_forward_workspace_bytes.
+ */
+int cce_logits_forward_backward(const void* logits, int logits_dtype, int64_t ld, const void* labels,
+                                int labels_int64, int64_t N, int64_t V, int64_t ignore_index, float label_smoothing,
+                                float z_loss_weight, int smoothing_form, int reduction, int grad_mean,
+                                float* loss_out, float* lse_out, int32_t* n_valid_out, void* grad_logits,
+                                int grad_dtype, int64_t ld_grad, void* workspace, size_t workspace_bytes,
+                                void* stream);
+
+/*
  * Per-kernel timing for measurement tools (no counterpart in the reference).
  * While enabled, every GEMM launch of cce_forward / cce_backward and every
- * row-kernel launch of cce_logits_forward / cce_logits_backward is bracketed
+ * row-kernel launch of cce_logits_forward / _backward / _forward_backward is bracketed
  * by HIP events recorded on its stream.  cce_kernel_timing_read() waits for
  * the recorded events and returns, for one kernel kind, the summed
  * milliseconds, the launch count and the work of those launches — credited
  * (the algorithmic work: forward logits, dHidden, dWeight; the backward's
  * logits recompute is executed but not credited) and executed — then clears
  * that kind's record.  The work is MFMA FLOPs for the GEMM kinds and
- * algorithmic HBM bytes for the two logits kinds.  credited_flops /
+ * algorithmic HBM bytes for the logits kinds.  credited_flops /
  * executed_flops may be NULL.  Kinds:
  */
 #define CCE_KERNEL_FWD_LSE 0   /* forward GEMM + online logsumexp                 */
@@ -186,7 +205,8 @@ int cce_logits_backward(const float* grad_out, const void* logits, int logits_dt
                                   of band b+1 in one launch                        */
 #define CCE_KERNEL_LOGITS_FWD 6 /* logits-in forward row kernel (reads N*V)     */
 #define CCE_KERNEL_LOGITS_BWD 7 /* logits-in backward row kernel (N*V in + out) */
-#define CCE_KERNEL_KINDS 8
+#define CCE_KERNEL_LOGITS_FUSED 8 /* logits-in loss + gradient kernel (N*V in + out) */
+#define CCE_KERNEL_KINDS 9
 int cce_kernel_timing_enable(int enable);
 int cce_kernel_timing_read(int kind, double* total_ms, int64_t* launches, double* credited_flops,
                            double* executed_flops);

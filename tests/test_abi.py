@@ -68,7 +68,8 @@ def test_constants_match_header():
                  "CCE_REDUCTION_NONE", "CCE_REDUCTION_MEAN", "CCE_REDUCTION_SUM", "CCE_DTYPE_BF16",
                  "CCE_DTYPE_F32", "CCE_DTYPE_F16", "CCE_SMOOTH_LOGV", "CCE_SMOOTH_UNIFORM", "CCE_KERNEL_FWD_LSE",
                  "CCE_KERNEL_BWD_GRAD", "CCE_KERNEL_BWD_DH", "CCE_KERNEL_BWD_DW", "CCE_KERNEL_BWD_DHDW",
-                 "CCE_KERNEL_BWD_BAND", "CCE_KERNEL_LOGITS_FWD", "CCE_KERNEL_LOGITS_BWD", "CCE_KERNEL_KINDS"):
+                 "CCE_KERNEL_BWD_BAND", "CCE_KERNEL_LOGITS_FWD", "CCE_KERNEL_LOGITS_BWD", "CCE_KERNEL_LOGITS_FUSED",
+                 "CCE_KERNEL_KINDS"):
         assert getattr(_lib, name) == header_define(name), name
     assert sorted(_lib.KERNEL_KIND_NAMES) == list(range(_lib.CCE_KERNEL_KINDS))
 

@@ -304,3 +304,85 @@ def test_overlapping_and_single_row_views_are_copied():
     l1 = m.chunked_cross_entropy_loss(xt, lab[:1])
     r1 = torch.nn.functional.cross_entropy(xt.float(), lab[:1])
     assert_loss_close(float(l1), float(r1), "strided single row")
+
+
+# ---------------------------------------------------------------------------
+# cce_logits_forward_backward: loss and gradient in one kernel
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype,f32", [(torch.bfloat16, False), (torch.bfloat16, True), (torch.float16, True),
+                                       (torch.float32, True)])
+@pytest.mark.parametrize("form", ["logv", "uniform"])
+@pytest.mark.parametrize("reduction,grad_mean", [("mean", True), ("mean", False), ("sum", False), ("none", False)])
+def test_fused_loss_and_gradient_kernel(dtype, f32, form, reduction, grad_mean):
+    from chronicals_amd import _lib
+    # N above the rows kept in flight (2 per CU), so workgroups take several rows; odd V
+    N, V = 3000, 20011
+    x, lab = _case(N, V, dtype, seed=71, oob=True)
+    code = _lib.CCE_SMOOTH_LOGV if form == "logv" else _lib.CCE_SMOOTH_UNIFORM
+    red = _lib.REDUCTIONS[reduction]
+    print(f"fused kernel dtype={dtype} f32={f32} form={form} reduction={reduction} grad_mean={grad_mean}", flush=True)
+    loss, lse, nv, dx = torch.ops.chronicals_hip.ce_logits_fwd_bwd(x.to(DEV), lab.to(DEV), IGNORE, 0.1, 1e-3, code,
+                                                                   red, grad_mean, f32)
+    rl, rlse, _ = oracle_ref(x, lab, 0.1, 1e-3, reduction, form)
+    gred = "mean" if grad_mean else "sum"
+    _, _, rg = oracle_ref(x, lab, 0.1, 1e-3, gred, form)
+    torch.cuda.synchronize()
+    assert dx.dtype == (torch.float32 if f32 else dtype)
+    assert int(nv) == int((lab != IGNORE).sum())
+    np.testing.assert_allclose(lse.cpu().numpy(), rlse, rtol=2e-5, atol=2e-5)
+    assert_loss_close(loss.cpu().numpy().reshape(np.shape(rl)), rl, "loss")
+    _check_grad(dx, rg, torch.float32 if dtype == torch.float32 else torch.bfloat16, "dlogits")
+
+
+def test_fused_kernel_in_place_matches_out_of_place_and_two_kernel_path():
+    from chronicals_amd import _lib
+    N, V = 1500, 32768
+    x, lab = _case(N, V, torch.bfloat16, seed=72)
+    xd, ld = x.to(DEV), lab.to(DEV)
+    l1, _, _, g1 = torch.ops.chronicals_hip.ce_logits_fwd_bwd(xd, ld, IGNORE, 0.2, 0.0, _lib.CCE_SMOOTH_UNIFORM,
+                                                              _lib.CCE_REDUCTION_MEAN, True, False)
+    xi = xd.clone()
+    l2, _, _ = torch.ops.chronicals_hip.ce_logits_fwd_bwd_(xi, ld, IGNORE, 0.2, 0.0, _lib.CCE_SMOOTH_UNIFORM,
+                                                           _lib.CCE_REDUCTION_MEAN, True)
+    torch.cuda.synchronize()
+    assert torch.equal(l1, l2) and torch.equal(g1, xi)
+    # the same numbers as forward + backward kernels (different reduction trees: ulp-level differences)
+    l3, lse3, nv3 = torch.ops.chronicals_hip.ce_logits_fwd(xd, ld, IGNORE, 0.2, 0.0, _lib.CCE_SMOOTH_UNIFORM,
+                                                           _lib.CCE_REDUCTION_MEAN)
+    g3 = torch.ops.chronicals_hip.ce_logits_bwd(torch.ones(1, device=DEV), xd, ld, lse3, nv3, IGNORE, 0.2, 0.0,
+                                                _lib.CCE_SMOOTH_UNIFORM, _lib.CCE_REDUCTION_MEAN, False)
+    torch.cuda.synchronize()
+    assert_loss_close(float(l1), float(l3), "loss", rtol=1e-6)
+    r = grad_report(g1.float().cpu().numpy(), g3.float().cpu().numpy())
+    assert r["frac"] <= 1e-2 and r["cos"] >= 1 - 1e-6, r
+
+
+def test_fused_kernel_ops_opcheck_and_determinism():
+    from torch.library import opcheck
+    from chronicals_amd import _lib
+    x, lab = _case(600, 5000, torch.bfloat16, seed=73)
+    xd, ld = x.to(DEV), lab.to(DEV)
+    for f32 in (False, True):
+        opcheck(torch.ops.chronicals_hip.ce_logits_fwd_bwd.default,
+                (xd, ld, IGNORE, 0.1, 1e-4, _lib.CCE_SMOOTH_UNIFORM, _lib.CCE_REDUCTION_MEAN, True, f32))
+    opcheck(torch.ops.chronicals_hip.ce_logits_fwd_bwd_.default,
+            (xd.clone(), ld, IGNORE, 0.1, 1e-4, _lib.CCE_SMOOTH_LOGV, _lib.CCE_REDUCTION_SUM, False))
+    a = torch.ops.chronicals_hip.ce_logits_fwd_bwd(xd, ld, IGNORE, 0.1, 1e-4, 1, 1, True, False)
+    b = torch.ops.chronicals_hip.ce_logits_fwd_bwd(xd, ld, IGNORE, 0.1, 1e-4, 1, 1, True, False)
+    torch.cuda.synchronize()
+    assert all(torch.equal(p, q) for p, q in zip(a, b))
+
+
+def test_fused_kernel_all_ignored_and_empty():
+    from chronicals_amd import _lib
+    x = torch.randn(700, 3000).to(DEV, torch.bfloat16)
+    lab = torch.full((700,), IGNORE, device=DEV)
+    loss, _, nv, g = torch.ops.chronicals_hip.ce_logits_fwd_bwd(x, lab, IGNORE, 0.1, 1e-2, 1, 1, True, True)
+    torch.cuda.synchronize()
+    assert float(loss) == 0.0 and int(nv) == 0 and not g.abs().sum().item()
+    e = torch.empty(0, 3000, device=DEV, dtype=torch.bfloat16)
+    loss, _, nv, g = torch.ops.chronicals_hip.ce_logits_fwd_bwd(e, torch.empty(0, dtype=torch.long, device=DEV),
+                                                                IGNORE, 0.0, 0.0, 0, 1, True, False)
+    torch.cuda.synchronize()
+    assert float(loss) == 0.0 and int(nv) == 0 and g.shape == (0, 3000)
