@@ -22,7 +22,6 @@ Tolerances: loss within 1e-3 relative; gradients with max abs error
 import copy
 import math
 
-import numpy as np
 import pytest
 import torch
 import torch.nn as nn
