@@ -2408,6 +2408,8 @@ int cce_logits_backward(const float* grad_out, const void* logits, int logits_dt
   if (grad_dtype != logits_dtype && grad_dtype != CCE_DTYPE_F32)
     return fail(CCE_ERR_INVALID_ARG, "grad_dtype must be the logits' dtype or CCE_DTYPE_F32, got %d", grad_dtype);
   if (ld_grad < V) return fail(CCE_ERR_INVALID_ARG, "gradient row stride %ld is smaller than V = %ld", (long)ld_grad, (long)V);
+  if (grad_logits == logits && (grad_dtype != logits_dtype || ld_grad != ld))
+    return fail(CCE_ERR_INVALID_ARG, "grad_logits may alias the logits only with the same dtype and row stride");
   if (N == 0) return CCE_OK;
   if (!grad_out || !logits || !labels || !lse || !n_valid || !grad_logits)
     return fail(CCE_ERR_INVALID_ARG, "grad_out, logits, labels, lse, n_valid and grad_logits must not be null");
@@ -2454,6 +2456,8 @@ int cce_logits_forward_backward(const void* logits, int logits_dtype, int64_t ld
   if (grad_dtype != logits_dtype && grad_dtype != CCE_DTYPE_F32)
     return fail(CCE_ERR_INVALID_ARG, "grad_dtype must be the logits' dtype or CCE_DTYPE_F32, got %d", grad_dtype);
   if (ld_grad < V) return fail(CCE_ERR_INVALID_ARG, "gradient row stride %ld is smaller than V = %ld", (long)ld_grad, (long)V);
+  if (grad_logits == logits && (grad_dtype != logits_dtype || ld_grad != ld))
+    return fail(CCE_ERR_INVALID_ARG, "grad_logits may alias the logits only with the same dtype and row stride");
   if (!n_valid_out || (!loss_out && (N > 0 || reduction != CCE_REDUCTION_NONE)) ||
       (N > 0 && (!logits || !labels || !lse_out || !grad_logits)))
     return fail(CCE_ERR_INVALID_ARG, "logits, labels, loss_out, lse_out, n_valid_out and grad_logits must not be null");

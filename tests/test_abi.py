@@ -204,3 +204,15 @@ def test_missing_library_fails_loudly(tmp_path):
     out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, cwd=REPO,
                          timeout=300)
     assert "IMPORT_ERROR" in out.stdout and "not found" in out.stdout, out.stdout + out.stderr
+
+
+def test_gradient_may_alias_logits_only_with_same_layout(lib):
+    fake = 0x10000
+    # fp32 gradient written over bf16 logits: refused before any launch
+    rc = lib.cce_logits_backward(fake, fake, _lib.CCE_DTYPE_BF16, 1000, fake, 1, fake, fake, 64, 1000, -100, 0.0, 0.0,
+                                 _lib.CCE_SMOOTH_LOGV, 1, fake, _lib.CCE_DTYPE_F32, 1000, None)
+    assert rc == _lib.CCE_ERR_INVALID_ARG and "alias" in lib.cce_last_error().decode()
+    rc = lib.cce_logits_forward_backward(fake, _lib.CCE_DTYPE_BF16, 1000, fake, 1, 64, 1000, -100, 0.0, 0.0,
+                                         _lib.CCE_SMOOTH_LOGV, 1, 1, fake, fake, fake, fake, _lib.CCE_DTYPE_BF16, 1024,
+                                         fake, 1 << 20, None)
+    assert rc == _lib.CCE_ERR_INVALID_ARG and "alias" in lib.cce_last_error().decode()
