@@ -386,3 +386,17 @@ def test_fused_kernel_all_ignored_and_empty():
                                                                 IGNORE, 0.0, 0.0, 0, 1, True, False)
     torch.cuda.synchronize()
     assert float(loss) == 0.0 and int(nv) == 0 and g.shape == (0, 3000)
+
+
+@pytest.mark.parametrize("scale", [300.0, 3000.0])
+def test_extreme_logit_magnitudes(scale):
+    # logits in the thousands: the online max keeps exp2 in range; float64 closed form as reference
+    m = _mod()
+    x, lab = _case(257, 4099, torch.float32, seed=81, scale=scale)
+    xd = x.to(DEV).requires_grad_(True)
+    loss = m.chunked_cross_entropy_loss(xd, lab.to(DEV), label_smoothing=0.1, z_loss_weight=1e-6)
+    loss.backward()
+    rl, _, rg = oracle_ref(x, lab, 0.1, 1e-6)
+    assert np.isfinite(float(loss.detach())) and torch.isfinite(xd.grad).all()
+    assert_loss_close(float(loss.detach()), float(rl), "loss")
+    _check_grad(xd.grad, rg, torch.bfloat16, "dlogits")

@@ -319,3 +319,18 @@ def test_peak_memory_bounded_by_chunk_at_C2(gpu):
           f"materialised fp32 logits + grad {N * V * 8 / 2**20:.0f} MiB", flush=True)
     assert peak <= bound
     assert peak < 0.1 * N * V * 8
+
+
+@pytest.mark.parametrize("scale", [30.0, 300.0])
+def test_fused_extreme_logit_magnitudes(gpu, scale):
+    """Large hidden norms (logits of order +-scale*sqrt(d)): the online log-sum-exp stays finite and exact."""
+    g = torch.Generator().manual_seed(82)
+    h = torch.randn(300, 128, generator=g) * scale
+    w = torch.randn(3001, 128, generator=g) * 0.1
+    lab = torch.randint(0, 3001, (300,), generator=g)
+    got = run_hip(gpu, h, w, lab, z=1e-6)
+    ref = run_oracle(h, w, lab, z=1e-6)
+    assert np.isfinite(got["loss"]).all()
+    assert_loss_close(got["loss"], ref["loss"], "loss")
+    assert_grad_close(got["dh"], ref["dh"], "dh")
+    assert_grad_close(got["dw"], ref["dw"], "dw")
