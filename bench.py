@@ -203,6 +203,10 @@ def main() -> int:
     w = w.to(torch.bfloat16).requires_grad_(not args.frozen_weight)
     N, d, V = cfg.N, cfg.d, cfg.V
     credited_step = (4.0 if args.frozen_weight else 6.0) * N * V * d
+    # the backward skips ignored rows (the forward still computes every row's
+    # log-sum-exp): the figure over labelled rows only is reported beside
+    n_valid = int((lab != -100).sum())
+    credited_valid = (4.0 if args.frozen_weight else 6.0) * n_valid * V * d
 
     def step():
         h.grad = None
@@ -288,6 +292,8 @@ def main() -> int:
                    "N": N, "d": d, "V": V, "chunk_size": args.chunk, "frozen_weight": bool(args.frozen_weight)},
         "pct_bf16_peak": 100.0 * step_tflops / PEAK_BF16_TFLOPS,
         "step_tflops_algorithmic": step_tflops,
+        "valid_rows": n_valid,
+        "pct_bf16_peak_valid_rows": 100.0 * credited_valid / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
                      # the chip runs below its 2.4 GHz peak clock under this load (power-limited); the
@@ -297,7 +303,8 @@ def main() -> int:
                      "kernel": f"{dom}: credited (algorithmic) FLOPs per launch "
                                f"({kd['credited_gflop_per_launch']:.1f} GFLOP) over its HIP-event average launch "
                                f"time ({kd['avg_launch_us']:.1f} us, {kd['launches_per_step']:g} launches/step); "
-                               f"executed incl. recompute {kd['tflops_executed']:.0f} TFLOP/s"},
+                               f"executed incl. recompute {kd['tflops_executed']:.0f} TFLOP/s; both count all N "
+                               f"rows; the backward GEMMs run only the row tiles holding the {n_valid} labelled rows"},
         "kernels": kernels,
         "peak_extra_mem_bytes": int(peak_extra),
         "loss": float(loss.item()),

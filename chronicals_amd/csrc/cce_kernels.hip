@@ -212,12 +212,20 @@ struct LoaderSel<false, 256, W> {
   typedef LoadMNMajor256<W> type;
 };
 
+// Row compaction: when `dyn` is set, `live` points at the device-side count
+// of live rows (a multiple of 256, or M).  kDynM: M is cut to it and the row
+// tiles past it do not run; kDynK: the reduction runs over the first `live`
+// rows only.
+constexpr int kDynNone = 0, kDynM = 1, kDynK = 2;
+
 struct GemmShape {
   const bf16_t* A;  // M x K operand
   long lda;
   const bf16_t* B;  // N x K operand
   long ldb;
   int M, N, K;
+  const int* live = nullptr;
+  int dyn = kDynNone;
 };
 
 // Accumulator tile of one wave: kWaveRows rows x (BN/2) columns as
@@ -709,6 +717,7 @@ struct AccParams {
   long ldo;
   int out_f32;  // 0: bf16 output, 1: fp32 output
   int mode;
+  const int* rowmap = nullptr;  // out row of GEMM row m (acc32 keeps GEMM rows); null: m
 };
 
 // Plain GEMM output with optional fp32 accumulation buffer.
@@ -750,11 +759,14 @@ struct EpiAcc {
           if (p.mode >= 2) v += *reinterpret_cast<const f32x4*>(p.acc32 + (long)m * p.ldacc + n);
           if (p.mode == 1 || p.mode == 2) {
             *reinterpret_cast<f32x4*>(p.acc32 + (long)m * p.ldacc + n) = v;
-          } else if (p.out_f32) {
-            *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + (long)m * p.ldo + n) = v;
           } else {
-            const u32x2 pk = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-            *reinterpret_cast<u32x2*>(reinterpret_cast<bf16_t*>(p.out) + (long)m * p.ldo + n) = pk;
+            const long om = p.rowmap ? (long)p.rowmap[m] : (long)m;
+            if (p.out_f32) {
+              *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + om * p.ldo + n) = v;
+            } else {
+              const u32x2 pk = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+              *reinterpret_cast<u32x2*>(reinterpret_cast<bf16_t*>(p.out) + om * p.ldo + n) = pk;
+            }
           }
         }
     }
@@ -790,9 +802,21 @@ constexpr int gemm_lds_elems(int pipe, int nst = 2) {
 }
 
 template <int BN, int W, bool AK, bool BKM, template <int, int> class EpiT, int PIPE, int NST = 2>
-__device__ __forceinline__ void gemm_body(const GemmShape& g, const typename EpiT<BN, W>::Params& ep, int bid,
+__device__ __forceinline__ void gemm_body(const GemmShape& g_in, const typename EpiT<BN, W>::Params& ep, int bid,
                                           int nb, bf16_t* smem) {
   typedef EpiT<BN, W> Epi;
+  GemmShape g = g_in;
+  if (g.dyn == kDynK) g.K = min(g.K, *g.live);
+  if (g.dyn == kDynM) {
+    // Only the row tiles below the live rows run, spread over the first
+    // nb * live_tiles / row_tiles workgroups (nb is a multiple of the row
+    // tile count for every row-dynamic launch), so that every XCD keeps an
+    // equal share; the remaining workgroups exit.
+    const int gm = (g.M + kBM - 1) / kBM;
+    g.M = min(g.M, *g.live);
+    nb = nb / gm * ((g.M + kBM - 1) / kBM);
+    if (bid >= nb) return;
+  }
   constexpr int kStage = (kBM + BN) * kPitch;
   // epilogue staging area, past the pipeline's LDS stages
   bf16_t* const scratch = smem + gemm_lds_elems<BN>(PIPE, NST);
@@ -1604,15 +1628,92 @@ __global__ __launch_bounds__(kFusedThreads) void ce_logits_fused_kernel(
   }
 }
 
-// Per-row backward coefficients.
+// Row compaction of the backward.  One workgroup partitions the rows: the
+// rows whose label is not ignore_index go first, in order (idx[0 .. cnt)),
+// the ignored ones after them (idx[cnt .. N), in reverse order).  live[0] =
+// min(N, 256 * max(1, ceil(cnt / 256))): the row tiles the backward GEMMs run
+// over; the ignored rows inside them carry zero coefficients.
+__global__ __launch_bounds__(1024) void compact_rows_kernel(const void* labels, int labels64, int N,
+                                                            long ignore_index, int* __restrict__ idx,
+                                                            int* __restrict__ live) {
+  __shared__ int wsum[2][16];
+  __shared__ int base[2];
+  const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
+  if (tid == 0) base[0] = base[1] = 0;
+  __syncthreads();
+  const uint64_t below = (l == 0) ? 0ull : (~0ull >> (64 - l));
+  for (int r0 = 0; r0 < N; r0 += 1024) {
+    const int n = r0 + tid;
+    const bool in = n < N;
+    const bool valid = in && load_label(labels, labels64, n) != ignore_index;
+    const uint64_t mv = __ballot(valid), mi = __ballot(in && !valid);
+    if (l == 0) {
+      wsum[0][w] = __popcll(mv);
+      wsum[1][w] = __popcll(mi);
+    }
+    __syncthreads();
+    int ov = base[0], oi = base[1];
+    for (int k = 0; k < w; ++k) {
+      ov += wsum[0][k];
+      oi += wsum[1][k];
+    }
+    if (valid) idx[ov + __popcll(mv & below)] = n;
+    else if (in) idx[N - 1 - (oi + __popcll(mi & below))] = n;
+    __syncthreads();
+    if (tid == 0) {
+      for (int k = 0; k < 16; ++k) {
+        base[0] += wsum[0][k];
+        base[1] += wsum[1][k];
+      }
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const long tiles = base[0] > 0 ? (base[0] + kBM - 1) / kBM : 1;
+    live[0] = (int)(tiles * kBM < N ? tiles * kBM : N);
+  }
+}
+
+// out[i][:] = H[idx[i]][:] for i < N (rows of d bf16, d a multiple of 8).
+__global__ __launch_bounds__(256) void gather_rows_kernel(const bf16_t* __restrict__ H, int d,
+                                                          const int* __restrict__ idx, int N,
+                                                          bf16_t* __restrict__ out) {
+  const int chunks = d >> 3;
+  const long total = (long)N * chunks;
+  for (long q = blockIdx.x * 256L + threadIdx.x; q < total; q += (long)gridDim.x * 256) {
+    const long i = q / chunks;
+    const int c = (int)(q - i * chunks);
+    *reinterpret_cast<u32x4*>(out + i * d + c * 8) =
+        *reinterpret_cast<const u32x4*>(H + (long)idx[i] * d + c * 8);
+  }
+}
+
+// Zero the rows idx[i], live[0] <= i < N, of a [N][d] output (row_bytes =
+// d * element size, a multiple of 16): the rows no backward GEMM writes.
+__global__ __launch_bounds__(256) void zero_rows_kernel(char* __restrict__ out, long row_bytes,
+                                                        const int* __restrict__ idx, const int* __restrict__ live,
+                                                        int N) {
+  const int first = live[0];
+  const long chunks = row_bytes >> 4;
+  const long total = (long)(N - first) * chunks;
+  for (long q = blockIdx.x * 256L + threadIdx.x; q < total; q += (long)gridDim.x * 256) {
+    const long i = first + q / chunks;
+    const long c = q % chunks;
+    *reinterpret_cast<u32x4*>(out + (long)idx[i] * row_bytes + c * 16) = u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+// Per-row backward coefficients, for GEMM row i of source row idx[i] (idx
+// null: i).
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__ grad_out,
                                                        const float* __restrict__ lse,
                                                        const int32_t* __restrict__ nvalid, const void* labels,
                                                        int labels64, int N, int V, long ignore_index, float eps,
-                                                       float zw, int reduction, float4* __restrict__ rowp,
-                                                       int* __restrict__ rowlab) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= N) return;
+                                                       float zw, int reduction, const int* __restrict__ idx,
+                                                       float4* __restrict__ rowp, int* __restrict__ rowlab) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= N) return;
+  const int n = idx ? idx[i] : i;
   const long lab = load_label(labels, labels64, n);
   const bool valid = (lab != ignore_index);
   float scale = 0.f;
@@ -1623,11 +1724,11 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__
   }
   if (valid) {
     const float L = lse[n];
-    rowp[n] = make_float4(L * kLog2e, scale * (1.f + 2.f * zw * L), scale * (1.f - eps), scale * eps / (float)V);
-    rowlab[n] = (lab >= 0 && lab < V) ? (int)lab : -1;
+    rowp[i] = make_float4(L * kLog2e, scale * (1.f + 2.f * zw * L), scale * (1.f - eps), scale * eps / (float)V);
+    rowlab[i] = (lab >= 0 && lab < V) ? (int)lab : -1;
   } else {
-    rowp[n] = make_float4(FLT_MAX, 0.f, 0.f, 0.f);
-    rowlab[n] = -1;
+    rowp[i] = make_float4(FLT_MAX, 0.f, 0.f, 0.f);
+    rowlab[i] = -1;
   }
 }
 
@@ -1663,11 +1764,13 @@ __global__ __launch_bounds__(256) void transpose_kernel(const bf16_t* __restrict
   }
 }
 
-// dB[c] = sum_m G[m][c] for c < C (fixed order: deterministic).  Block = 64 columns.
+// dB[c] = sum_m G[m][c] for c < C (fixed order: deterministic).  Block = 64
+// columns.  With `live`, M = min(M, live[0]).
 __global__ __launch_bounds__(256) void colsum_kernel(const bf16_t* __restrict__ G, long ldg, int M, int C,
-                                                     float* __restrict__ out) {
+                                                     const int* __restrict__ live, float* __restrict__ out) {
   // blockIdx.y = row split: rows [y*M/gridDim.y, (y+1)*M/gridDim.y) into out[y][C]
   __shared__ float part[32][65];
+  if (live) M = min(M, live[0]);
   const int tid = threadIdx.x;
   const int cg = tid & 7, rg = tid >> 3;  // 8 column groups of 8, 32 row groups
   const int c0 = blockIdx.x * 64 + cg * 8;
@@ -1832,6 +1935,10 @@ struct BwdLayout {
   bf16_t* WT;
   bf16_t* HT;
   float* dHacc;
+  // row compaction (banded backward): row order, live row count, H in that order
+  int* idx;
+  int* live;
+  bf16_t* Hc;
   size_t bytes;
 };
 
@@ -1851,6 +1958,10 @@ BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bo
   L.WT = need_dh ? c.take<bf16_t>((size_t)d * Vb) : nullptr;
   L.HT = need_dw ? c.take<bf16_t>((size_t)d * N8) : nullptr;
   L.dHacc = (need_dh && nbands > 1) ? c.take<float>((size_t)N * d) : nullptr;
+  const bool compact = banded(d);
+  L.idx = compact ? c.take<int>((size_t)N) : nullptr;
+  L.live = compact ? c.take<int>(1) : nullptr;
+  L.Hc = compact ? c.take<bf16_t>((size_t)N * d) : nullptr;
   L.bytes = align_up(c.off, 256);
   return L;
 }
@@ -1972,8 +2083,9 @@ int launch_acc(const GemmShape& g, const AccParams& ep, hipStream_t st, int kind
 void grad_shape(const bf16_t* H, const bf16_t* W, const float* bias, const BwdLayout& L, bf16_t* G, long N, long d,
                 long Vb, long v0, long vb, int bn, GemmShape& g, GradParams& e, int& nb) {
   const int gm = (int)ceil_div(N, kBM);
-  g.A = H; g.lda = d; g.B = W + v0 * d; g.ldb = d;
+  g.A = L.Hc ? L.Hc : H; g.lda = d; g.B = W + v0 * d; g.ldb = d;
   g.M = (int)N; g.N = (int)vb; g.K = (int)d;
+  g.live = L.live; g.dyn = L.live ? kDynM : kDynNone;
   e.bias = bias; e.rowp = L.rowp; e.rowlab = L.rowlab; e.G = G; e.ldg = Vb; e.v0 = (int)v0;
   e.tiles_n = (int)ceil_div(vb, bn);
   e.splits = (int)std::min<long>(e.tiles_n, std::max<long>(1, ceil_div(CCE_GRAD_WGS, gm)));
@@ -2129,7 +2241,7 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
   const bool uniform = smoothing_form == CCE_SMOOTH_UNIFORM && label_smoothing > 0.f;
   if (uniform) {
     hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)ceil_div(d, 64), (unsigned)L.wsplits), dim3(256), 0, st,
-                       static_cast<const bf16_t*>(weight), (long)d, (int)V, (int)d, L.wpart);
+                       static_cast<const bf16_t*>(weight), (long)d, (int)V, (int)d, nullptr, L.wpart);
     HIP_TRY(hipGetLastError());
     hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)ceil_div(d, 256)), dim3(256), 0, st, L.wpart, L.wsplits,
                        (int)d, bias, (int)V, L.wsum);
@@ -2190,13 +2302,30 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
   const bf16_t* H = static_cast<const bf16_t*>(hidden);
   const bf16_t* W = static_cast<const bf16_t*>(weight);
 
+  // Banded backward: the rows with a label are compacted to the front (the
+  // GEMMs then skip the row tiles past them); the rest of dH is zeroed here.
+  if (L.idx) {
+    hipLaunchKernelGGL(compact_rows_kernel, dim3(1), dim3(1024), 0, st, labels, labels_int64, (int)N,
+                       (long)ignore_index, L.idx, L.live);
+    HIP_TRY(hipGetLastError());
+    const long chunks = (long)N * (d / 8);
+    hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)std::min<long>(ceil_div(chunks, 256), 8192)), dim3(256), 0,
+                       st, H, (int)d, L.idx, (int)N, L.Hc);
+    HIP_TRY(hipGetLastError());
+    if (need_dh) {
+      const long row_bytes = d * (grad_hidden_dtype == CCE_DTYPE_F32 ? 4 : 2);
+      hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)std::min<long>(ceil_div(N * (row_bytes / 16), 256), 4096)),
+                         dim3(256), 0, st, static_cast<char*>(grad_hidden), row_bytes, L.idx, L.live, (int)N);
+      HIP_TRY(hipGetLastError());
+    }
+  }
   hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)ceil_div(N, 256)), dim3(256), 0, st, grad_out, lse, n_valid,
                      labels, labels_int64, (int)N, (int)V, (long)ignore_index, label_smoothing, z_loss_weight,
-                     reduction, L.rowp, L.rowlab);
+                     reduction, L.idx, L.rowp, L.rowlab);
   HIP_TRY(hipGetLastError());
   if (need_dw) {
     hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)ceil_div(N8, 64), (unsigned)ceil_div(d, 64)), dim3(256), 0,
-                       st, H, (long)d, (int)N, (int)d, L.HT, (long)N8, (int)N8);
+                       st, L.Hc ? L.Hc : H, (long)d, (int)N, (int)d, L.HT, (long)N8, (int)N8);
     HIP_TRY(hipGetLastError());
   }
 
@@ -2213,6 +2342,8 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     band_cols(b, v0, vb, vb64);
     g.A = G; g.lda = Vb; g.B = L.WT + c0 * Vb; g.ldb = Vb;
     g.M = (int)N; g.N = (int)nc; g.K = (int)vb64;
+    g.live = L.live; g.dyn = L.live ? kDynM : kDynNone;
+    e.rowmap = L.idx;
     e.acc32 = L.dHacc ? L.dHacc + c0 : nullptr; e.ldacc = d;
     e.out = (grad_hidden_dtype == CCE_DTYPE_F32) ? static_cast<void*>(static_cast<float*>(grad_hidden) + c0)
                                                  : static_cast<void*>(static_cast<bf16_t*>(grad_hidden) + c0);
@@ -2228,6 +2359,8 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     g.A = G; g.lda = Vb;  // MN-major: element (v, n) at G[n*Vb + v]
     g.B = L.HT + c0 * N8; g.ldb = N8;
     g.M = (int)vb; g.N = (int)nc; g.K = (int)N;
+    g.live = L.live; g.dyn = L.live ? kDynK : kDynNone;
+    e.rowmap = nullptr;
     e.acc32 = nullptr; e.ldacc = 0;
     const long o = v0 * d + c0;
     e.out = (grad_weight_dtype == CCE_DTYPE_F32) ? static_cast<void*>(static_cast<float*>(grad_weight) + o)
@@ -2249,7 +2382,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     long v0, vb, vb64;
     band_cols(b, v0, vb, vb64);
     hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)ceil_div(vb, 64)), dim3(256), 0, st, G, (long)Vb, (int)N,
-                       (int)vb, grad_bias + v0);
+                       (int)vb, L.live, grad_bias + v0);
     HIP_TRY(hipGetLastError());
     return CCE_OK;
   };

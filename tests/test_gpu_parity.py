@@ -127,6 +127,39 @@ def test_all_ignored(gpu):
     assert not np.any(got["dh"]) and not np.any(got["dw"]) and not np.any(got["db"])
 
 
+@pytest.mark.parametrize("reduction,bias,hdtype", [("mean", True, torch.bfloat16), ("none", False, torch.float32),
+                                                    ("sum", True, torch.float32)])
+def test_ignored_row_tiles_are_skipped(gpu, reduction, bias, hdtype):
+    # The banded backward compacts the labelled rows to the front and skips
+    # the 256-row tiles past them: 400 labelled rows of 1100 leave 2 of 5 row
+    # tiles live.  The ignored rows' dH must still be exactly zero.
+    print(f"case compaction reduction={reduction} bias={bias} hdtype={hdtype}", flush=True)
+    h, w, lab, b = _rand_case(1100, 128, 3000, seed=21, ignore_frac=0.0, bias=bias)
+    g = torch.Generator().manual_seed(4)
+    lab[torch.randperm(1100, generator=g)[:700]] = IGNORE
+    go = torch.rand(1100, generator=g) if reduction == "none" else 1.3
+    got = run_hip(gpu, h, w, lab, b, chunk=1024, reduction=reduction, grad_output=go, hdtype=hdtype)
+    ref = run_oracle(h, w, lab, b, chunk=1024, reduction=reduction, grad_output=go)
+    compare(got, ref, f"compaction {reduction}")
+    ign = (lab == IGNORE).numpy()
+    assert not np.any(got["dh"][ign])
+
+
+def test_all_ignored_many_row_tiles(gpu):
+    h, w, lab, b = _rand_case(1000, 64, 700, seed=19, bias=True)
+    lab[:] = IGNORE
+    got = run_hip(gpu, h, w, lab, b, chunk=256)
+    assert float(got["loss"]) == 0.0
+    assert not np.any(got["dh"]) and not np.any(got["dw"]) and not np.any(got["db"])
+
+
+def test_labelled_rows_at_the_end(gpu):
+    # the labelled rows sit in the last row tile; compaction moves them to the first
+    h, w, lab, _ = _rand_case(900, 192, 2500, seed=23, ignore_frac=0.0)
+    lab[:850] = IGNORE
+    compare(run_hip(gpu, h, w, lab, chunk=512), run_oracle(h, w, lab, chunk=512), "tail rows")
+
+
 def test_empty_batch(gpu):
     h = torch.zeros(0, 64)
     w = torch.randn(300, 64) * 0.02
