@@ -59,7 +59,7 @@ constexpr int kWarp8 = 8;
 constexpr int kFastBN = 256;    // PIPE 4 kernels
 constexpr int kSlowBN = 128;    // PIPE 3 kernels
 #ifndef CCE_GRAD_WGS
-#define CCE_GRAD_WGS 1024  // target workgroups of a recompute launch
+#define CCE_GRAD_WGS 1024  // target workgroups of a recompute launch of its own
 #endif
 
 constexpr int kBM = 256;              // rows of a workgroup tile
@@ -2080,15 +2080,19 @@ int launch_acc(const GemmShape& g, const AccParams& ep, hipStream_t st, int kind
 }
 
 // Recompute launch shape of one band: G[n][c] for columns [v0, v0 + vb).
+// A recompute launch of its own runs each workgroup over a run of column
+// tiles (about CCE_GRAD_WGS workgroups: fewer pipeline restarts); inside the
+// band launch (`in_band`) each workgroup takes one tile, the finest grain for
+// filling the CUs that the long dW / dH tiles leave idle.
 void grad_shape(const bf16_t* H, const bf16_t* W, const float* bias, const BwdLayout& L, bf16_t* G, long N, long d,
-                long Vb, long v0, long vb, int bn, GemmShape& g, GradParams& e, int& nb) {
+                long Vb, long v0, long vb, int bn, bool in_band, GemmShape& g, GradParams& e, int& nb) {
   const int gm = (int)ceil_div(N, kBM);
   g.A = L.Hc ? L.Hc : H; g.lda = d; g.B = W + v0 * d; g.ldb = d;
   g.M = (int)N; g.N = (int)vb; g.K = (int)d;
   g.live = L.live; g.dyn = L.live ? kDynM : kDynNone;
   e.bias = bias; e.rowp = L.rowp; e.rowlab = L.rowlab; e.G = G; e.ldg = Vb; e.v0 = (int)v0;
   e.tiles_n = (int)ceil_div(vb, bn);
-  e.splits = (int)std::min<long>(e.tiles_n, std::max<long>(1, ceil_div(CCE_GRAD_WGS, gm)));
+  e.splits = in_band ? e.tiles_n : (int)std::min<long>(e.tiles_n, std::max<long>(1, ceil_div(CCE_GRAD_WGS, gm)));
   nb = gm * e.splits;
 }
 
@@ -2397,7 +2401,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       GemmShape g1 = {};
       GradParams e1 = {};
       int nb1 = 0;
-      grad_shape(H, W, bias, L, L.G[0], N, d, Vb, v0, vb, kFastBN, g1, e1, nb1);
+      grad_shape(H, W, bias, L, L.G[0], N, d, Vb, v0, vb, kFastBN, false, g1, e1, nb1);
       rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiGradBias, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false)
                 : launch_gemm<kFastBN, kWarp8, true, true, EpiGrad, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false);
       if (rc) return rc;
@@ -2430,7 +2434,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       if (b + 1 < nbands) {
         long v0, vb, vb64;
         band_cols(b + 1, v0, vb, vb64);
-        grad_shape(H, W, bias, L, L.G[(b + 1) & 1], N, d, Vb, v0, vb, kFastBN, p.gr, p.e_gr, p.nb_gr);
+        grad_shape(H, W, bias, L, L.G[(b + 1) & 1], N, d, Vb, v0, vb, kFastBN, true, p.gr, p.e_gr, p.nb_gr);
       }
       rc = launch_band(p, bias != nullptr, st);
       if (rc) return rc;
@@ -2450,7 +2454,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     GemmShape g1 = {};
     GradParams e1 = {};
     int nb1 = 0;
-    grad_shape(H, W, bias, L, L.G[0], N, d, Vb, v0, vb, kSlowBN, g1, e1, nb1);
+    grad_shape(H, W, bias, L, L.G[0], N, d, Vb, v0, vb, kSlowBN, false, g1, e1, nb1);
     rc = bias ? launch_gemm<kSlowBN, kWarp8, true, true, EpiGradBias, 3>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false)
               : launch_gemm<kSlowBN, kWarp8, true, true, EpiGrad, 3>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false);
     if (rc) return rc;
