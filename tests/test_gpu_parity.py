@@ -11,8 +11,8 @@ import pytest
 import torch
 
 from oracle import cce_oracle as oracle
-from tests.cce_common import (CONFIGS, IGNORE, assert_grad_close, assert_loss_close, bf16_exact, grad_report,
-                              make_inputs, torch_reference)
+from tests.cce_common import (CONFIGS, IGNORE, assert_grad_close, assert_grad_close_torch, assert_loss_close,
+                              bf16_exact, grad_report_torch, make_inputs, torch_reference_rows)
 
 pytestmark = pytest.mark.gpu
 
@@ -246,19 +246,25 @@ def test_deterministic(gpu):
         assert np.array_equal(a[k], c[k]), k
 
 
-@pytest.mark.parametrize("name", ["C2"])
+@pytest.mark.parametrize("name", ["C2", "C3", "C4", "C5"])
 def test_full_size_vs_torch_fp32(gpu, name):
-    """Full configuration against a materialised-logits fp32 torch reference on the GPU."""
+    """Every benchmark configuration at full size against an fp32 torch
+    reference that materialises the logits (4096 rows at a time) on the GPU,
+    from the same bf16-rounded inputs."""
     cfg = CONFIGS[name]
     print(f"case {name} full vs torch fp32", flush=True)
     h, w, lab = make_inputs(cfg, seed=0, device=gpu, gen_device="cuda")
-    got = run_hip(gpu, h, w, lab)
-    ref = torch_reference(bf16_exact(h), bf16_exact(w), lab, dtype=torch.float32)
-    rep = {k: grad_report(got[k], ref[k].cpu().numpy()) for k in ("dh", "dw")}
-    print(f"{name} loss {float(got['loss']):.6f} ref {float(ref['loss']):.6f} {rep}", flush=True)
-    assert_loss_close(got["loss"], ref["loss"].cpu().numpy(), f"{name} loss")
-    assert_grad_close(got["dh"], ref["dh"].cpu().numpy(), f"{name} dh")
-    assert_grad_close(got["dw"], ref["dw"].cpu().numpy(), f"{name} dw")
+    hd = h.detach().to(torch.bfloat16).requires_grad_(True)
+    wd = w.detach().to(torch.bfloat16).requires_grad_(True)
+    loss = _cce()(hd, wd, lab, None, 8192, IGNORE, 0.0, 0.0, reduction=cfg.reduction)
+    loss.backward()
+    torch.cuda.synchronize()
+    ref = torch_reference_rows(hd.detach(), wd.detach(), lab, dtype=torch.float32)
+    rep = {"dh": grad_report_torch(hd.grad, ref["dh"]), "dw": grad_report_torch(wd.grad, ref["dw"])}
+    print(f"{name} loss {float(loss.detach()):.6f} ref {float(ref['loss']):.6f} {rep}", flush=True)
+    assert_loss_close(float(loss.detach()), float(ref["loss"]), f"{name} loss")
+    assert_grad_close_torch(hd.grad, ref["dh"], f"{name} dh")
+    assert_grad_close_torch(wd.grad, ref["dw"], f"{name} dw")
 
 
 def test_custom_ops_opcheck(gpu):
