@@ -1102,6 +1102,18 @@ __global__ __launch_bounds__(W * 64) void dual_acc_kernel(GemmShape g_dw, AccPar
 // then the short recompute tiles, which fill the CUs the long tiles leave
 // idle at the end of the band.  The 128-wide tail tiles fit three LDS stages
 // (two slabs in flight) in the space the 256-wide tiles use for two.
+// The transpose of the next band's W rows (dH's B operand) rides along as the
+// last, shortest population: one 64 x 64 tile per workgroup.
+struct TransposeParams {
+  const bf16_t* in;
+  long ldi;
+  int R, C;
+  bf16_t* out;
+  long ldo;
+  int Rpad;
+  int tiles_r;  // 64-row tiles of in
+};
+
 struct BandLaunch {
   GemmShape dw;
   AccParams e_dw;
@@ -1113,8 +1125,13 @@ struct BandLaunch {
   AccParams e_dh2;
   GemmShape gr;
   GradParams e_gr;
-  int nb_dw, nb_dw2, nb_dh, nb_dh2, nb_gr;
+  TransposeParams tr;
+  int nb_dw, nb_dw2, nb_dh, nb_dh2, nb_gr, nb_tr;
 };
+
+template <int NT>
+__device__ inline void transpose_tile(const bf16_t* __restrict__ in, long ldi, int R, int C, bf16_t* __restrict__ out,
+                                      long ldo, int Rpad, int r0, int c0, bf16_t (*t)[66], int tid);
 
 template <bool HB>
 __global__ __launch_bounds__(kWarp8 * 64) void band_kernel(BandLaunch p) {
@@ -1140,10 +1157,16 @@ __global__ __launch_bounds__(kWarp8 * 64) void band_kernel(BandLaunch p) {
     return;
   }
   b -= p.nb_dh2;
-  if constexpr (HB)
-    gemm_body<kFastBN, kWarp8, true, true, EpiGradBias, 4>(p.gr, p.e_gr, b, p.nb_gr, smem);
-  else
-    gemm_body<kFastBN, kWarp8, true, true, EpiGrad, 4>(p.gr, p.e_gr, b, p.nb_gr, smem);
+  if (b < p.nb_gr) {
+    if constexpr (HB)
+      gemm_body<kFastBN, kWarp8, true, true, EpiGradBias, 4>(p.gr, p.e_gr, b, p.nb_gr, smem);
+    else
+      gemm_body<kFastBN, kWarp8, true, true, EpiGrad, 4>(p.gr, p.e_gr, b, p.nb_gr, smem);
+    return;
+  }
+  b -= p.nb_gr;
+  transpose_tile<kWarp8 * 64>(p.tr.in, p.tr.ldi, p.tr.R, p.tr.C, p.tr.out, p.tr.ldo, p.tr.Rpad, (b % p.tr.tiles_r) * 64,
+                              (b / p.tr.tiles_r) * 64, reinterpret_cast<bf16_t(*)[66]>(smem), threadIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1732,15 +1755,14 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__
   }
 }
 
-// out[c][r] = in[r][c] for r < R (zero for R <= r < Rpad), c < C.  64x64 tiles.
-__global__ __launch_bounds__(256) void transpose_kernel(const bf16_t* __restrict__ in, long ldi, int R, int C,
-                                                        bf16_t* __restrict__ out, long ldo, int Rpad) {
-  __shared__ bf16_t t[64][66];
-  const int r0 = blockIdx.x * 64, c0 = blockIdx.y * 64;
-  const int tid = threadIdx.x;
+// out[c][r] = in[r][c] for r < R (zero for R <= r < Rpad), c < C, over the
+// 64 x 64 tile at (r0, c0), by NT threads staging through t.
+template <int NT>
+__device__ inline void transpose_tile(const bf16_t* __restrict__ in, long ldi, int R, int C, bf16_t* __restrict__ out,
+                                      long ldo, int Rpad, int r0, int c0, bf16_t (*t)[66], int tid) {
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int q = tid + it * 256;        // 512 chunks of 8 elements
+  for (int it = 0; it < 512 / NT; ++it) {
+    const int q = tid + it * NT;         // 512 chunks of 8 elements
     const int rr = q >> 3, cc = (q & 7) * 8;
     u32x4 v = u32x4{0u, 0u, 0u, 0u};
     if (r0 + rr < R && c0 + cc < C) v = *reinterpret_cast<const u32x4*>(in + (long)(r0 + rr) * ldi + c0 + cc);
@@ -1752,8 +1774,8 @@ __global__ __launch_bounds__(256) void transpose_kernel(const bf16_t* __restrict
   }
   __syncthreads();
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int q = tid + it * 256;
+  for (int it = 0; it < 512 / NT; ++it) {
+    const int q = tid + it * NT;
     const int cc = q >> 3, rr = (q & 7) * 8;
     if (c0 + cc < C && r0 + rr < Rpad) {
       u32x4 v;
@@ -1762,6 +1784,12 @@ __global__ __launch_bounds__(256) void transpose_kernel(const bf16_t* __restrict
       *reinterpret_cast<u32x4*>(out + (long)(c0 + cc) * ldo + r0 + rr) = v;
     }
   }
+}
+
+__global__ __launch_bounds__(256) void transpose_kernel(const bf16_t* __restrict__ in, long ldi, int R, int C,
+                                                        bf16_t* __restrict__ out, long ldo, int Rpad) {
+  __shared__ bf16_t t[64][66];
+  transpose_tile<256>(in, ldi, R, C, out, ldo, Rpad, blockIdx.x * 64, blockIdx.y * 64, t, threadIdx.x);
 }
 
 // dB[c] = sum_m G[m][c] for c < C (fixed order: deterministic).  Block = 64
@@ -1931,8 +1959,8 @@ FwdLayout fwd_layout(void* ws, long N, long d, long V, int reduction) {
 struct BwdLayout {
   float4* rowp;
   int* rowlab;
-  bf16_t* G[2];  // band gradient buffers; the second only when bands alternate
-  bf16_t* WT;
+  bf16_t* G[2];   // band gradient buffers; the second only when bands alternate
+  bf16_t* WT[2];  // W band transposes; the second only when bands alternate
   bf16_t* HT;
   float* dHacc;
   // row compaction (banded backward): row order, live row count, H in that order
@@ -1955,7 +1983,8 @@ BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bo
   L.rowlab = c.take<int>((size_t)N);
   L.G[0] = c.take<bf16_t>((size_t)N * Vb);
   L.G[1] = (banded(d) && nbands > 1) ? c.take<bf16_t>((size_t)N * Vb) : L.G[0];
-  L.WT = need_dh ? c.take<bf16_t>((size_t)d * Vb) : nullptr;
+  L.WT[0] = need_dh ? c.take<bf16_t>((size_t)d * Vb) : nullptr;
+  L.WT[1] = (need_dh && banded(d) && nbands > 1) ? c.take<bf16_t>((size_t)d * Vb) : L.WT[0];
   L.HT = need_dw ? c.take<bf16_t>((size_t)d * N8) : nullptr;
   L.dHacc = (need_dh && nbands > 1) ? c.take<float>((size_t)N * d) : nullptr;
   const bool compact = banded(d);
@@ -2097,7 +2126,7 @@ void grad_shape(const bf16_t* H, const bf16_t* W, const float* bias, const BwdLa
 }
 
 int launch_band(const BandLaunch& p, bool has_bias, hipStream_t st) {
-  const int nb = p.nb_dw + p.nb_dw2 + p.nb_dh + p.nb_dh2 + p.nb_gr;
+  const int nb = p.nb_dw + p.nb_dw2 + p.nb_dh + p.nb_dh2 + p.nb_gr + p.nb_tr;
   if (nb <= 0) return CCE_OK;
   hipEvent_t t0 = nullptr, t1 = nullptr;
   const bool timed = timing_begin(st, &t0, &t1);
@@ -2344,7 +2373,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
   auto dh_shape = [&](long b, const bf16_t* G, long c0, long nc, GemmShape& g, AccParams& e) {
     long v0, vb, vb64;
     band_cols(b, v0, vb, vb64);
-    g.A = G; g.lda = Vb; g.B = L.WT + c0 * Vb; g.ldb = Vb;
+    g.A = G; g.lda = Vb; g.B = L.WT[b & 1] + c0 * Vb; g.ldb = Vb;
     g.M = (int)N; g.N = (int)nc; g.K = (int)vb64;
     g.live = L.live; g.dyn = L.live ? kDynM : kDynNone;
     e.rowmap = L.idx;
@@ -2373,12 +2402,21 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     e.out_f32 = (grad_weight_dtype == CCE_DTYPE_F32);
     e.mode = 0;
   };
-  // WT[j][c] = W[v0 + c][j], zero for vb <= c < vb64
-  auto transpose_band = [&](long b) -> int {
+  // WT[b & 1][j][c] = W[v0 + c][j], zero for vb <= c < vb64: as its own
+  // launch, or as the transpose population of the previous band's launch
+  auto transpose_params = [&](long b, TransposeParams& t) -> int {
     long v0, vb, vb64;
     band_cols(b, v0, vb, vb64);
-    hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)ceil_div(vb64, 64), (unsigned)ceil_div(d, 64)), dim3(256), 0,
-                       st, W + v0 * d, (long)d, (int)vb, (int)d, L.WT, (long)Vb, (int)vb64);
+    t.in = W + v0 * d; t.ldi = d; t.R = (int)vb; t.C = (int)d;
+    t.out = L.WT[b & 1]; t.ldo = Vb; t.Rpad = (int)vb64;
+    t.tiles_r = (int)ceil_div(vb64, 64);
+    return t.tiles_r * (int)ceil_div(d, 64);
+  };
+  auto transpose_band = [&](long b) -> int {
+    TransposeParams t;
+    const int tiles = transpose_params(b, t);
+    hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)t.tiles_r, (unsigned)(tiles / t.tiles_r)), dim3(256), 0, st,
+                       t.in, t.ldi, t.R, t.C, t.out, t.ldo, t.Rpad);
     HIP_TRY(hipGetLastError());
     return CCE_OK;
   };
@@ -2405,6 +2443,10 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiGradBias, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false)
                 : launch_gemm<kFastBN, kWarp8, true, true, EpiGrad, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false);
       if (rc) return rc;
+      if (need_dh) {
+        rc = transpose_band(0);
+        if (rc) return rc;
+      }
     }
     for (long b = 0; b < nbands; ++b) {
       const bf16_t* G = L.G[b & 1];
@@ -2420,8 +2462,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
         }
       }
       if (need_dh) {
-        rc = transpose_band(b);
-        if (rc) return rc;
+        if (b + 1 < nbands) p.nb_tr = transpose_params(b + 1, p.tr);  // into the other WT buffer
         if (dmain > 0) {
           dh_shape(b, G, 0, dmain, p.dh, p.e_dh);
           p.nb_dh = gm * (int)ceil_div(dmain, kFastBN);
