@@ -11,7 +11,7 @@ import threading
 from . import build as _build
 
 # constants mirrored from include/chronicals_cce.h
-CCE_ABI_VERSION = 3
+CCE_ABI_VERSION = 4
 CCE_OK = 0
 CCE_ERR_INVALID_ARG = 1
 CCE_ERR_WORKSPACE = 2
@@ -24,6 +24,8 @@ CCE_DTYPE_F32 = 1
 CCE_DTYPE_F16 = 2
 CCE_SMOOTH_LOGV = 0
 CCE_SMOOTH_UNIFORM = 1
+CCE_LSE_ALL_ROWS = 0
+CCE_LSE_LABELLED_ROWS = 1
 
 CCE_KERNEL_FWD_LSE = 0
 CCE_KERNEL_BWD_GRAD = 1
@@ -52,12 +54,12 @@ _sz = ctypes.c_size_t
 SIGNATURES = {
     "cce_abi_version": (_i32, []),
     "cce_last_error": (ctypes.c_char_p, []),
-    "cce_forward_workspace_bytes": (_i32, [_i64, _i64, _i64, _i32, ctypes.POINTER(_sz)]),
+    "cce_forward_workspace_bytes": (_i32, [_i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_sz)]),
     "cce_backward_workspace_bytes": (_i32, [_i64, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_sz)]),
     "cce_forward": (_i32, [
         _vp, _vp, _vp, _i32, _vp,            # hidden, weight, labels, labels_int64, bias
         _i64, _i64, _i64, _i64,              # N, d, V, ignore_index
-        _f32, _f32, _i32, _i32,              # label_smoothing, z_loss_weight, smoothing_form, reduction
+        _f32, _f32, _i32, _i32, _i32,        # label_smoothing, z_loss_weight, smoothing_form, reduction, lse_rows
         _vp, _vp, _vp, _vp,                  # loss_out, lse_out, target_out, n_valid_out
         _vp, _sz, _vp,                       # workspace, workspace_bytes, stream
     ]),
@@ -140,9 +142,9 @@ def check(rc: int) -> None:
         raise CCEError(f"libchronicals_cce error {rc}: {msg.decode() if msg else ''}")
 
 
-def forward_workspace_bytes(N: int, d: int, V: int, reduction: int) -> int:
+def forward_workspace_bytes(N: int, d: int, V: int, reduction: int, lse_rows: int = CCE_LSE_ALL_ROWS) -> int:
     out = _sz(0)
-    check(load().cce_forward_workspace_bytes(N, d, V, reduction, ctypes.byref(out)))
+    check(load().cce_forward_workspace_bytes(N, d, V, reduction, lse_rows, ctypes.byref(out)))
     return out.value
 
 

@@ -417,11 +417,17 @@ __device__ inline void mfma_frags(const Frags<BN, W>& f, WaveAcc<BN, W>& acc) {
 
 struct LseParams {
   const float* bias;  // [V] or null
-  float* pm;          // [splits][M] running max (log2 units)
-  float* ps;          // [splits][M] sum of 2^(x - max)
+  float* pm;          // [splits][ldp] running max (log2 units)
+  float* ps;          // [splits][ldp] sum of 2^(x - max)
+  long ldp;           // row stride of pm / ps
   int splits;
   int tiles_n;
 };
+
+// Vocabulary splits per row tile of a forward whose rows were compacted:
+// all nb workgroups share the gl live row tiles, so the split count and the
+// partials' row stride (whole live tiles) follow the device-side live count.
+__device__ inline int lse_dyn_splits(int nb, int gl, int tiles_n) { return max(1, min(nb / gl, tiles_n)); }
 
 // Forward: per-row online (max, sum-exp) in base 2 over the workgroup's run of
 // vocabulary tiles; at the end one partial per (row, split) is written.
@@ -429,6 +435,7 @@ template <int BN, int W, bool HB>
 struct EpiLseT {
   typedef LseParams Params;
   static constexpr bool kMultiTile = true;
+  static constexpr bool kDynSplits = true;
   static constexpr int FM = WaveCfg<W>::kFM;
   struct State {
     float m[FM], s[FM];
@@ -436,11 +443,16 @@ struct EpiLseT {
   static __device__ inline void assign(const GemmShape& g, const Params& p, int bid, int nb, int& tm,
                                        int& t0, int& t1, int& split) {
     const int gm = (g.M + kBM - 1) / kBM;
+    const int S = g.dyn == kDynM ? lse_dyn_splits(nb, gm, p.tiles_n) : p.splits;
+    if (bid >= gm * S) {  // a compacted forward uses gm * S of the nb workgroups
+      t0 = t1 = 0;
+      return;
+    }
     int s;
-    grouped_map<8>(bid, nb, gm, p.splits, tm, s);
+    grouped_map<8>(bid, gm * S, gm, S, tm, s);
     split = s;
-    t0 = (int)(((long)p.tiles_n * s) / p.splits);
-    t1 = (int)(((long)p.tiles_n * (s + 1)) / p.splits);
+    t0 = (int)(((long)p.tiles_n * s) / S);
+    t1 = (int)(((long)p.tiles_n * (s + 1)) / S);
   }
   static constexpr int kStores = 0;  // global stores a tile epilogue issues per wave
   static __device__ inline void init(const Params&, State& st, const GemmShape&, int, int, int) {
@@ -534,8 +546,9 @@ struct EpiLseT {
         merge(st.m[i], st.s[i], red[row], red[kBM + row]);
         const int grow = tm * kBM + row;
         if (grow < g.M) {
-          p.pm[(long)split * g.M + grow] = st.m[i];
-          p.ps[(long)split * g.M + grow] = st.s[i];
+          const long ldp = g.dyn == kDynM ? (long)(g.M + kBM - 1) / kBM * kBM : p.ldp;
+          p.pm[(long)split * ldp + grow] = st.m[i];
+          p.ps[(long)split * ldp + grow] = st.s[i];
         }
       }
     }
@@ -573,6 +586,7 @@ struct EpiGradT {
   // Each workgroup walks a run of column tiles of one row tile, so the next
   // tile's loads are in flight while this tile's epilogue runs.
   static constexpr bool kMultiTile = true;
+  static constexpr bool kDynSplits = false;
   static constexpr int FM = WaveCfg<W>::kFM;
   static constexpr int kScratch = W * 2048;  // 32 x 64 bf16 per wave
   // Without bias the tile epilogue issues exactly kStores buffer stores per
@@ -727,6 +741,7 @@ template <int BN, int W>
 struct EpiAcc {
   typedef AccParams Params;
   static constexpr bool kMultiTile = false;
+  static constexpr bool kDynSplits = false;
   static constexpr int FM = WaveCfg<W>::kFM;
   static constexpr int kScratch = 0;
   struct State {};
@@ -808,14 +823,18 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g_in, const typename 
   GemmShape g = g_in;
   if (g.dyn == kDynK) g.K = min(g.K, *g.live);
   if (g.dyn == kDynM) {
-    // Only the row tiles below the live rows run, spread over the first
-    // nb * live_tiles / row_tiles workgroups (nb is a multiple of the row
-    // tile count for every row-dynamic launch), so that every XCD keeps an
-    // equal share; the remaining workgroups exit.
+    // Only the row tiles below the live rows run.  Epilogues with
+    // kDynSplits re-split the vocabulary over all nb workgroups themselves;
+    // otherwise the live tiles are spread over the first nb * live_tiles /
+    // row_tiles workgroups (nb is a multiple of the row tile count for every
+    // row-dynamic launch), so that every XCD keeps an equal share, and the
+    // remaining workgroups exit.
     const int gm = (g.M + kBM - 1) / kBM;
     g.M = min(g.M, *g.live);
-    nb = nb / gm * ((g.M + kBM - 1) / kBM);
-    if (bid >= nb) return;
+    if constexpr (!Epi::kDynSplits) {
+      nb = nb / gm * ((g.M + kBM - 1) / kBM);
+      if (bid >= nb) return;
+    }
   }
   constexpr int kStage = (kBM + BN) * kPitch;
   // epilogue staging area, past the pipeline's LDS stages
@@ -1183,33 +1202,49 @@ __device__ inline long load_label(const void* labels, int is64, long n) {
 __global__ __launch_bounds__(256) void fwd_combine_kernel(
     const float* __restrict__ pm, const float* __restrict__ ps, int splits, const bf16_t* __restrict__ H,
     const bf16_t* __restrict__ W, const void* labels, int labels64, const float* __restrict__ bias, int N, int d,
-    int V, long ignore_index, float eps, float zw, float logV, const float* __restrict__ wsum,
-    float* __restrict__ lse_out, float* __restrict__ target_out, float* __restrict__ rowloss,
-    float* __restrict__ bsum, int* __restrict__ bcnt) {
+    int V, long ignore_index, float eps, float zw, float logV, const float* __restrict__ wsum, int labelled_only,
+    const int* __restrict__ idx, const int* __restrict__ live, int nb_fwd, int tiles_n, float* __restrict__ lse_out,
+    float* __restrict__ target_out, float* __restrict__ rowloss, float* __restrict__ bsum, int* __restrict__ bcnt) {
+  // wave w handles partial row i; its source row is idx[i] (identity without
+  // idx).  With labelled_only, ignored rows get lse 0 and their partials,
+  // which the compacted GEMM may not have written, are not read.  A
+  // compacted forward (live set) split the vocabulary into
+  // lse_dyn_splits(nb_fwd, live tiles, tiles_n) parts with whole live tiles
+  // as the partials' row stride.
   const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int n = blockIdx.x * 4 + w;
+  const int i = blockIdx.x * 4 + w;
+  long ldp = N;
+  if (live) {
+    const int gl = (live[0] + kBM - 1) / kBM;
+    splits = lse_dyn_splits(nb_fwd, gl, tiles_n);
+    ldp = (long)gl * kBM;
+  }
   __shared__ float s_loss[4];
   __shared__ int s_cnt[4];
   float loss = 0.f;
   int cnt = 0;
-  if (n < N) {
-    float m = kNegBig, s = 0.f;
-    for (int k = l; k < splits; k += 64) {
-      const float m2 = pm[(long)k * N + n], s2 = ps[(long)k * N + n];
-      const float mn = fmaxf(m, m2);
-      s = s * fast_exp2(m - mn) + s2 * fast_exp2(m2 - mn);
-      m = mn;
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
-      const float mn = fmaxf(m, m2);
-      s = s * exp2f(m - mn) + s2 * exp2f(m2 - mn);
-      m = mn;
-    }
-    const float lse = m * kLn2 + logf(s + 1e-10f);
+  if (i < N) {
+    const int n = idx ? idx[i] : i;
     const long lab = load_label(labels, labels64, n);
     const bool valid = (lab != ignore_index);
+    float lse = 0.f;
+    if (valid || !labelled_only) {
+      float m = kNegBig, s = 0.f;
+      for (int k = l; k < splits; k += 64) {
+        const float m2 = pm[(long)k * ldp + i], s2 = ps[(long)k * ldp + i];
+        const float mn = fmaxf(m, m2);
+        s = s * fast_exp2(m - mn) + s2 * fast_exp2(m2 - mn);
+        m = mn;
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
+        const float mn = fmaxf(m, m2);
+        s = s * exp2f(m - mn) + s2 * exp2f(m2 - mn);
+        m = mn;
+      }
+      lse = m * kLn2 + logf(s + 1e-10f);
+    }
     float t = 0.f;
     if (valid && lab >= 0 && lab < V) {
       const bf16_t* h = H + (long)n * d;
@@ -1900,10 +1935,15 @@ struct Carver {
 bool fast_k(long K) { return K % 64 == 0; }
 int lse_bn(long d) { return fast_k(d) ? kFastBN : kSlowBN; }
 
-int forward_splits(long N, long d, long V) {
+// A compacted forward re-splits the vocabulary over the live row tiles on
+// the device (lse_dyn_splits): at least 32 splits per row tile keep each
+// workgroup short, so the partly filled last wave of workgroups left when
+// some row tiles drop out costs little.
+int forward_splits(long N, long d, long V, bool compact) {
   if (N <= 0) return 1;
   const long gm = ceil_div(N, kBM), tn = ceil_div(V, lse_bn(d));
   long s = ceil_div(2048, gm);
+  if (compact && s < 32) s = 32;
   if (s > tn) s = tn;
   if (s < 1) s = 1;
   return (int)s;
@@ -1927,6 +1967,11 @@ struct FwdLayout {
   int* bcnt;
   float *wpart, *wsum;  // column sums of W by row split, and their total (+ the bias sum)
   int wsplits;
+  // row compaction (CCE_LSE_LABELLED_ROWS, d a multiple of 64): row order,
+  // live row count, H in that order
+  int* idx;
+  int* live;
+  bf16_t* Hc;
   size_t bytes;
 };
 
@@ -1939,19 +1984,30 @@ int wsum_splits(long d, long V) {
   return (int)(r < rows ? r : (rows > 0 ? rows : 1));
 }
 
-FwdLayout fwd_layout(void* ws, long N, long d, long V, int reduction) {
+// The forward compacts its rows when only the labelled rows' lse is wanted
+// and the direct-to-LDS GEMM runs (d a multiple of 64).
+bool fwd_compacts(long d, int lse_rows) { return lse_rows == CCE_LSE_LABELLED_ROWS && fast_k(d); }
+
+FwdLayout fwd_layout(void* ws, long N, long d, long V, int reduction, int lse_rows) {
   Carver c(ws);
   FwdLayout L;
-  const int S = forward_splits(N, d, V);
+  const bool compact = fwd_compacts(d, lse_rows) && N > 0;
+  const int S = forward_splits(N, d, V, compact);
   const long nb = ceil_div(N, 4);
-  L.pm = c.take<float>((size_t)S * N);
-  L.ps = c.take<float>((size_t)S * N);
+  // [S][N] partials, or for a compacted forward up to nb = S * row tiles
+  // workgroup slots of 256 rows each
+  const size_t parts = (size_t)S * (size_t)ceil_div(N > 0 ? N : 1, kBM) * kBM;
+  L.pm = c.take<float>(parts);
+  L.ps = c.take<float>(parts);
   L.bsum = c.take<float>((size_t)(nb > 0 ? nb : 1));
   L.bcnt = c.take<int>((size_t)(nb > 0 ? nb : 1));
   L.rowloss = (reduction == CCE_REDUCTION_NONE) ? nullptr : c.take<float>((size_t)(N > 0 ? N : 1));
   L.wsplits = wsum_splits(d, V);
   L.wpart = c.take<float>((size_t)L.wsplits * d);
   L.wsum = c.take<float>((size_t)d + 1);
+  L.idx = compact ? c.take<int>((size_t)N) : nullptr;
+  L.live = compact ? c.take<int>(1) : nullptr;
+  L.Hc = compact ? c.take<bf16_t>((size_t)N * d) : nullptr;
   L.bytes = align_up(c.off, 256);
   return L;
 }
@@ -2195,14 +2251,16 @@ const char* cce_last_error(void) { return g_err; }
 
 int cce_abi_version(void) { return CCE_ABI_VERSION; }
 
-int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, size_t* bytes) {
+int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, int lse_rows, size_t* bytes) {
   g_err[0] = 0;
   if (!bytes) return fail(CCE_ERR_INVALID_ARG, "bytes must not be null");
   int rc = check_dims(N, d, V);
   if (rc) return rc;
   if (reduction < CCE_REDUCTION_NONE || reduction > CCE_REDUCTION_SUM)
     return fail(CCE_ERR_INVALID_ARG, "reduction must be 0 (none), 1 (mean) or 2 (sum), got %d", reduction);
-  *bytes = fwd_layout(nullptr, N, d, V, reduction).bytes;
+  if (lse_rows != CCE_LSE_ALL_ROWS && lse_rows != CCE_LSE_LABELLED_ROWS)
+    return fail(CCE_ERR_INVALID_ARG, "lse_rows must be CCE_LSE_ALL_ROWS or CCE_LSE_LABELLED_ROWS, got %d", lse_rows);
+  *bytes = fwd_layout(nullptr, N, d, V, reduction, lse_rows).bytes;
   return CCE_OK;
 }
 
@@ -2218,7 +2276,7 @@ int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_
 
 int cce_forward(const void* hidden, const void* weight, const void* labels, int labels_int64, const float* bias,
                 int64_t N, int64_t d, int64_t V, int64_t ignore_index, float label_smoothing, float z_loss_weight,
-                int smoothing_form, int reduction, float* loss_out, float* lse_out, float* target_out,
+                int smoothing_form, int reduction, int lse_rows, float* loss_out, float* lse_out, float* target_out,
                 int32_t* n_valid_out, void* workspace, size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
   int rc = check_dims(N, d, V);
@@ -2228,6 +2286,8 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
                 smoothing_form);
   if (reduction < CCE_REDUCTION_NONE || reduction > CCE_REDUCTION_SUM)
     return fail(CCE_ERR_INVALID_ARG, "reduction must be 0 (none), 1 (mean) or 2 (sum), got %d", reduction);
+  if (lse_rows != CCE_LSE_ALL_ROWS && lse_rows != CCE_LSE_LABELLED_ROWS)
+    return fail(CCE_ERR_INVALID_ARG, "lse_rows must be CCE_LSE_ALL_ROWS or CCE_LSE_LABELLED_ROWS, got %d", lse_rows);
   if (!n_valid_out || (!loss_out && !(reduction == CCE_REDUCTION_NONE && N == 0)))
     return fail(CCE_ERR_INVALID_ARG, "loss_out and n_valid_out must not be null");
   if (N > 0 && (!hidden || !weight || !labels || !lse_out))
@@ -2237,7 +2297,7 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
   if (misaligned(hidden) || misaligned(weight) || misaligned(workspace))
     return fail(CCE_ERR_INVALID_ARG, "hidden, weight and workspace must be 16-byte aligned");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const FwdLayout need = fwd_layout(nullptr, N, d, V, reduction);
+  const FwdLayout need = fwd_layout(nullptr, N, d, V, reduction, lse_rows);
   if (workspace_bytes < need.bytes || (need.bytes && !workspace))
     return fail(CCE_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need.bytes, workspace_bytes);
   if (N == 0) {
@@ -2245,22 +2305,37 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
     if (!rc && reduction != CCE_REDUCTION_NONE) rc = zero_fill(loss_out, sizeof(float), st);
     return rc;
   }
-  const FwdLayout L = fwd_layout(workspace, N, d, V, reduction);
-  const int S = forward_splits(N, d, V);
+  const FwdLayout L = fwd_layout(workspace, N, d, V, reduction, lse_rows);
+  const int S = forward_splits(N, d, V, L.idx != nullptr);
   const int gm = (int)ceil_div(N, kBM);
 
+  // CCE_LSE_LABELLED_ROWS: the labelled rows go first and the GEMM runs only
+  // over the row tiles that hold them (the partials then follow that order)
+  if (L.idx) {
+    hipLaunchKernelGGL(compact_rows_kernel, dim3(1), dim3(1024), 0, st, labels, labels_int64, (int)N,
+                       (long)ignore_index, L.idx, L.live);
+    HIP_TRY(hipGetLastError());
+    const long chunks = (long)N * (d / 8);
+    hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)std::min<long>(ceil_div(chunks, 256), 8192)), dim3(256), 0,
+                       st, static_cast<const bf16_t*>(hidden), (int)d, L.idx, (int)N, L.Hc);
+    HIP_TRY(hipGetLastError());
+  }
+
   GemmShape g;
-  g.A = static_cast<const bf16_t*>(hidden);
+  g.A = L.Hc ? L.Hc : static_cast<const bf16_t*>(hidden);
   g.lda = d;
   g.B = static_cast<const bf16_t*>(weight);
   g.ldb = d;
   g.M = (int)N;
   g.N = (int)V;
   g.K = (int)d;
+  g.live = L.live;
+  g.dyn = L.live ? kDynM : kDynNone;
   LseParams ep;
   ep.bias = bias;
   ep.pm = L.pm;
   ep.ps = L.ps;
+  ep.ldp = N;
   ep.splits = S;
   ep.tiles_n = (int)ceil_div(V, lse_bn(d));
   if (fast_k(d))
@@ -2286,7 +2361,8 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
   hipLaunchKernelGGL(fwd_combine_kernel, dim3(nb), dim3(256), 0, st, L.pm, L.ps, S,
                      static_cast<const bf16_t*>(hidden), static_cast<const bf16_t*>(weight), labels, labels_int64,
                      bias, (int)N, (int)d, (int)V, (long)ignore_index, label_smoothing, z_loss_weight, logV,
-                     uniform ? L.wsum : nullptr, lse_out, target_out, rowloss, L.bsum, L.bcnt);
+                     uniform ? L.wsum : nullptr, lse_rows == CCE_LSE_LABELLED_ROWS, L.idx, L.live, gm * S,
+                     ep.tiles_n, lse_out, target_out, rowloss, L.bsum, L.bcnt);
   HIP_TRY(hipGetLastError());
   hipLaunchKernelGGL(fwd_finalize_kernel, dim3(1), dim3(1024), 0, st, L.bsum, L.bcnt, nb, reduction, loss_out,
                      n_valid_out);

@@ -119,12 +119,14 @@ def _reduction_code(reduction: str) -> int:
 
 
 def _forward_raw(hidden, weight, labels, bias, ignore_index, label_smoothing, z_loss_weight, red,
-                 smoothing_form=_lib.CCE_SMOOTH_LOGV):
+                 smoothing_form=_lib.CCE_SMOOTH_LOGV, lse_rows=_lib.CCE_LSE_ALL_ROWS):
     """Operand preparation + one chronicals_hip::cce_fwd call.
 
     Returns (loss, lse, n_valid, h2, w2, lab, b32, target): the bf16 [N, d] /
     [V, d] operands, flat labels and fp32 bias the backward reuses, and the
-    per-row target logits.
+    per-row target logits.  With lse_rows = CCE_LSE_LABELLED_ROWS the ignored
+    rows' lse and target are 0 and the forward skips their share of the
+    logits GEMM; callers that only use labelled rows' lse pass it.
     """
     _validate(hidden, weight, labels, bias)
     d = hidden.shape[-1]
@@ -136,7 +138,7 @@ def _forward_raw(hidden, weight, labels, bias, ignore_index, label_smoothing, z_
     b32 = None if bias is None else bias.detach().to(torch.float32).contiguous()
     loss, lse, n_valid, target = torch.ops.chronicals_hip.cce_fwd(h2, w2, lab, b32, int(ignore_index),
                                                                   float(label_smoothing), float(z_loss_weight),
-                                                                  int(smoothing_form), int(red))
+                                                                  int(smoothing_form), int(red), int(lse_rows))
     return loss, lse, n_valid, h2, w2, lab, b32, target
 
 
@@ -153,7 +155,8 @@ class CutCrossEntropyFunction(torch.autograd.Function):
                 reduction="mean"):
         red = _reduction_code(reduction)
         loss, lse, n_valid, h2, w2, lab, b32, _ = _forward_raw(hidden, weight, labels, bias, ignore_index,
-                                                               label_smoothing, z_loss_weight, red)
+                                                               label_smoothing, z_loss_weight, red,
+                                                               lse_rows=_lib.CCE_LSE_LABELLED_ROWS)
         ctx.save_for_backward(h2, w2, lab, lse, n_valid, b32)
         ctx.cfg = (int(chunk_size), int(ignore_index), float(label_smoothing), float(z_loss_weight), red)
         ctx.shapes = (hidden.shape, hidden.dtype, weight.dtype, None if bias is None else bias.dtype)
@@ -189,7 +192,8 @@ def _backward_raw(ctx, grad_output, need_dh, need_dw, need_db):
 
 
 class _LinearCE(torch.autograd.Function):
-    """(loss, lse) of the fused kernels; lse carries no gradient.
+    """(loss, lse) of the fused kernels; lse carries no gradient and is 0 on
+    ignored rows (the forward skips them).
 
     apply(hidden, weight, labels, bias, chunk_size, ignore_index, eps, z,
           reduction_code, smoothing_form)
@@ -198,7 +202,7 @@ class _LinearCE(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden, weight, labels, bias, chunk_size, ignore_index, eps, z, red, form):
         loss, lse, n_valid, h2, w2, lab, b32, _ = _forward_raw(hidden, weight, labels, bias, ignore_index, eps, z, red,
-                                                            form)
+                                                            form, _lib.CCE_LSE_LABELLED_ROWS)
         ctx.save_for_backward(h2, w2, lab, lse, n_valid, b32)
         ctx.cfg = (int(chunk_size), int(ignore_index), float(eps), float(z), red)
         ctx.shapes = (hidden.shape, hidden.dtype, weight.dtype, None if bias is None else bias.dtype)
@@ -384,7 +388,7 @@ def compute_z_loss(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Ten
     """
     del chunk_size
     _, lse, _, _, _, lab, _, _ = _forward_raw(hidden, weight, labels, bias, ignore_index, 0.0, 0.0,
-                                              _lib.CCE_REDUCTION_MEAN)
+                                              _lib.CCE_REDUCTION_MEAN, lse_rows=_lib.CCE_LSE_LABELLED_ROWS)
     valid = (lab != ignore_index).to(torch.float32)
     return (lse * lse * valid).sum() / valid.sum().clamp(min=1)
 

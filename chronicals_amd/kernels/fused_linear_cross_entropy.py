@@ -133,7 +133,8 @@ class FusedLinearCrossEntropyFunction(torch.autograd.Function):
     def forward(ctx, hidden, weight, bias, labels, label_smoothing, z_loss_weight, ignore_index, chunk_size):
         red = _lib.CCE_REDUCTION_MEAN
         loss, lse, n_valid, h2, w2, lab, b32, _ = _forward_raw(hidden, weight, labels, bias, ignore_index,
-                                                            label_smoothing, z_loss_weight, red)
+                                                            label_smoothing, z_loss_weight, red,
+                                                            lse_rows=_lib.CCE_LSE_LABELLED_ROWS)
         ctx.save_for_backward(h2, w2, lab, lse, n_valid, b32)
         ctx.cfg = (int(chunk_size), int(ignore_index), float(label_smoothing), float(z_loss_weight), red)
         ctx.shapes = (hidden.shape, hidden.dtype, weight.dtype, None if bias is None else bias.dtype)
@@ -233,7 +234,7 @@ def triton_fused_linear_cross_entropy_forward(
     with torch.no_grad():
         loss, lse, n_valid, h2, w2, lab, b32, _ = _forward_raw(hidden, weight, target, bias, ignore_index,
                                                             label_smoothing, lse_square_scale, red,
-                                                            _lib.CCE_SMOOTH_UNIFORM)
+                                                            _lib.CCE_SMOOTH_UNIFORM, _lib.CCE_LSE_LABELLED_ROWS)
         gred = _lib.CCE_REDUCTION_SUM if red == _lib.CCE_REDUCTION_NONE else red
         one = torch.ones((1,), dtype=torch.float32, device=h2.device)
         dh, dw, db = torch.ops.chronicals_hip.cce_bwd(
@@ -260,7 +261,7 @@ class TritonFusedLinearCrossEntropyFunction(torch.autograd.Function):
         red = _reduction_code(reduction)
         loss, lse, n_valid, h2, w2, lab, b32, _ = _forward_raw(hidden, weight, target, bias, ignore_index,
                                                             label_smoothing, lse_scale, red,
-                                                            _lib.CCE_SMOOTH_UNIFORM)
+                                                            _lib.CCE_SMOOTH_UNIFORM, _lib.CCE_LSE_LABELLED_ROWS)
         ctx.save_for_backward(h2, w2, lab, lse, n_valid, b32)
         ctx.cfg = (int(chunk_size), int(ignore_index), float(label_smoothing), float(lse_scale), red)
         ctx.shapes = (hidden.shape, hidden.dtype, weight.dtype, None if bias is None else bias.dtype)

@@ -67,8 +67,8 @@ def _check_operands(hidden: Tensor, weight: Tensor, labels: Tensor, bias: Option
 
 @torch.library.custom_op("chronicals_hip::cce_fwd", mutates_args=(), device_types="cuda")
 def cce_fwd(hidden: Tensor, weight: Tensor, labels: Tensor, bias: Optional[Tensor], ignore_index: int,
-            label_smoothing: float, z_loss_weight: float, smoothing_form: int,
-            reduction: int) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+            label_smoothing: float, z_loss_weight: float, smoothing_form: int, reduction: int,
+            lse_rows: int = _lib.CCE_LSE_ALL_ROWS) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
     _check_operands(hidden, weight, labels, bias)
     hidden, weight = _aligned(hidden), _aligned(weight)
     lib = _lib.load()
@@ -76,7 +76,8 @@ def cce_fwd(hidden: Tensor, weight: Tensor, labels: Tensor, bias: Optional[Tenso
     N, d = hidden.shape
     V = weight.shape[0]
     with torch.cuda.device(device):
-        ws = torch.empty(_lib.forward_workspace_bytes(N, d, V, reduction), dtype=torch.uint8, device=device)
+        ws = torch.empty(_lib.forward_workspace_bytes(N, d, V, reduction, lse_rows), dtype=torch.uint8,
+                         device=device)
         loss = torch.empty((N,) if reduction == _lib.CCE_REDUCTION_NONE else (1,), dtype=torch.float32,
                            device=device)
         lse = torch.empty((N,), dtype=torch.float32, device=device)
@@ -86,14 +87,14 @@ def cce_fwd(hidden: Tensor, weight: Tensor, labels: Tensor, bias: Optional[Tenso
             hidden.data_ptr(), weight.data_ptr(), labels.data_ptr(), int(labels.dtype == torch.int64),
             bias.data_ptr() if bias is not None else None,
             N, d, V, int(ignore_index), float(label_smoothing), float(z_loss_weight), int(smoothing_form),
-            int(reduction), loss.data_ptr(), lse.data_ptr(), target.data_ptr(), n_valid.data_ptr(),
+            int(reduction), int(lse_rows), loss.data_ptr(), lse.data_ptr(), target.data_ptr(), n_valid.data_ptr(),
             ws.data_ptr(), ws.numel(), _stream(device)))
     return loss, lse, n_valid, target
 
 
 @cce_fwd.register_fake
 def _cce_fwd_fake(hidden, weight, labels, bias, ignore_index, label_smoothing, z_loss_weight, smoothing_form,
-                  reduction):
+                  reduction, lse_rows=_lib.CCE_LSE_ALL_ROWS):
     N = hidden.shape[0]
     loss = hidden.new_empty((N,) if reduction == _lib.CCE_REDUCTION_NONE else (1,), dtype=torch.float32)
     return (loss, hidden.new_empty((N,), dtype=torch.float32), hidden.new_empty((1,), dtype=torch.int32),

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define CCE_ABI_VERSION 3
+#define CCE_ABI_VERSION 4
 
 #define CCE_OK 0
 #define CCE_ERR_INVALID_ARG 1
@@ -61,6 +61,14 @@ extern "C" {
 #define CCE_SMOOTH_UNIFORM 1 /* eps*(lse - mean_v x), the uniform-target CE
                                 (triton_kernels.py:189-193, :2915, :2952-2956)               */
 
+/* rows of cce_forward's lse_out / target_out: every row, as
+   CutCrossEntropyForward.forward returns (cut_cross_entropy.py:671, :692), or
+   only the rows with a label (ignored rows read 0), which lets the forward
+   skip the ignored rows' share of the logits GEMM.  The loss, n_valid and
+   everything cce_backward reads are the same either way. */
+#define CCE_LSE_ALL_ROWS 0
+#define CCE_LSE_LABELLED_ROWS 1
+
 /* Library ABI version (CCE_ABI_VERSION).  No reference counterpart. */
 int cce_abi_version(void);
 
@@ -68,7 +76,7 @@ int cce_abi_version(void);
 const char* cce_last_error(void);
 
 /* Workspace bytes cce_forward needs for this problem. */
-int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, size_t* bytes);
+int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, int lse_rows, size_t* bytes);
 
 /*
  * Forward.  Replaces CutCrossEntropyForward.forward
@@ -87,11 +95,15 @@ int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, 
  *                   and labels outside [0, V) (:663-668); may be NULL
  * lse_out [N] fp32 is what cce_backward consumes (the reference saves it at
  * :841).  loss_out holds 1 float (mean/sum) or N floats (none).  Both
- * smoothing forms have the gradient cce_backward computes.
+ * smoothing forms have the gradient cce_backward computes.  lse_rows
+ * (CCE_LSE_ALL_ROWS / CCE_LSE_LABELLED_ROWS) selects whether ignored rows get
+ * their lse and target logit or 0; with CCE_LSE_LABELLED_ROWS and d a
+ * multiple of 64 the logits GEMM runs only over the 256-row tiles that hold
+ * labelled rows.
  */
 int cce_forward(const void* hidden, const void* weight, const void* labels, int labels_int64,
                 const float* bias, int64_t N, int64_t d, int64_t V, int64_t ignore_index,
-                float label_smoothing, float z_loss_weight, int smoothing_form, int reduction,
+                float label_smoothing, float z_loss_weight, int smoothing_form, int reduction, int lse_rows,
                 float* loss_out, float* lse_out, float* target_out, int32_t* n_valid_out,
                 void* workspace, size_t workspace_bytes, void* stream);
 

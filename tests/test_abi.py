@@ -66,7 +66,8 @@ def test_no_undeclared_exports():
 def test_constants_match_header():
     for name in ("CCE_ABI_VERSION", "CCE_OK", "CCE_ERR_INVALID_ARG", "CCE_ERR_WORKSPACE", "CCE_ERR_HIP",
                  "CCE_REDUCTION_NONE", "CCE_REDUCTION_MEAN", "CCE_REDUCTION_SUM", "CCE_DTYPE_BF16",
-                 "CCE_DTYPE_F32", "CCE_DTYPE_F16", "CCE_SMOOTH_LOGV", "CCE_SMOOTH_UNIFORM", "CCE_KERNEL_FWD_LSE",
+                 "CCE_DTYPE_F32", "CCE_DTYPE_F16", "CCE_SMOOTH_LOGV", "CCE_SMOOTH_UNIFORM", "CCE_LSE_ALL_ROWS",
+                 "CCE_LSE_LABELLED_ROWS", "CCE_KERNEL_FWD_LSE",
                  "CCE_KERNEL_BWD_GRAD", "CCE_KERNEL_BWD_DH", "CCE_KERNEL_BWD_DW", "CCE_KERNEL_BWD_DHDW",
                  "CCE_KERNEL_BWD_BAND", "CCE_KERNEL_LOGITS_FWD", "CCE_KERNEL_LOGITS_BWD", "CCE_KERNEL_LOGITS_FUSED",
                  "CCE_KERNEL_KINDS"):
@@ -125,29 +126,49 @@ def test_workspace_queries(lib):
 ])
 def test_workspace_query_rejects_bad_arguments(lib, N, d, V, red, msg):
     out = ctypes.c_size_t(0)
-    rc = lib.cce_forward_workspace_bytes(N, d, V, red, ctypes.byref(out))
+    rc = lib.cce_forward_workspace_bytes(N, d, V, red, _lib.CCE_LSE_ALL_ROWS, ctypes.byref(out))
     assert rc == _lib.CCE_ERR_INVALID_ARG
     assert msg in lib.cce_last_error().decode()
+
+
+def test_lse_rows_option(lib):
+    out = ctypes.c_size_t(0)
+    assert lib.cce_forward_workspace_bytes(64, 64, 1000, 1, 2, ctypes.byref(out)) == _lib.CCE_ERR_INVALID_ARG
+    assert "lse_rows" in lib.cce_last_error().decode()
+    fake = 0x10000
+    rc = lib.cce_forward(fake, fake, fake, 1, None, 64, 64, 1000, -100, 0.0, 0.0, _lib.CCE_SMOOTH_LOGV,
+                         _lib.CCE_REDUCTION_MEAN, 7, fake, fake, None, fake, fake, 1 << 30, None)
+    assert rc == _lib.CCE_ERR_INVALID_ARG and "lse_rows" in lib.cce_last_error().decode()
+    # labelled rows only: with d a multiple of 64 the forward reorders the rows (row order and a copy of
+    # the hidden rows in the workspace); with any other d it needs nothing more
+    sizes = {}
+    for d in (64, 72):
+        for rows in (_lib.CCE_LSE_ALL_ROWS, _lib.CCE_LSE_LABELLED_ROWS):
+            assert lib.cce_forward_workspace_bytes(300, d, 1000, 1, rows, ctypes.byref(out)) == _lib.CCE_OK
+            sizes[d, rows] = out.value
+    assert sizes[64, 1] >= sizes[64, 0] + 300 * 64 * 2 + 300 * 4
+    assert sizes[72, 1] == sizes[72, 0]
 
 
 def test_forward_rejects_small_workspace_before_launch(lib):
     fake = 0x10000  # never dereferenced: validation fails first
     rc = lib.cce_forward(fake, fake, fake, 1, None, 64, 64, 1000, -100, 0.0, 0.0, _lib.CCE_SMOOTH_LOGV,
-                         _lib.CCE_REDUCTION_MEAN, fake, fake, None, fake, fake, 16, None)
+                         _lib.CCE_REDUCTION_MEAN, _lib.CCE_LSE_ALL_ROWS, fake, fake, None, fake, fake, 16, None)
     assert rc == _lib.CCE_ERR_WORKSPACE
     assert "workspace too small" in lib.cce_last_error().decode()
 
 
 def test_forward_rejects_null_inputs(lib):
     rc = lib.cce_forward(None, None, None, 1, None, 64, 64, 1000, -100, 0.0, 0.0, _lib.CCE_SMOOTH_LOGV,
-                         _lib.CCE_REDUCTION_MEAN, 0x10000, 0x10000, None, 0x10000, 0x10000, 1 << 20, None)
+                         _lib.CCE_REDUCTION_MEAN, _lib.CCE_LSE_ALL_ROWS, 0x10000, 0x10000, None, 0x10000, 0x10000,
+                         1 << 20, None)
     assert rc == _lib.CCE_ERR_INVALID_ARG
 
 
 def test_forward_rejects_bad_smoothing_form(lib):
     fake = 0x10000
     rc = lib.cce_forward(fake, fake, fake, 1, None, 64, 64, 1000, -100, 0.1, 0.0, 2, _lib.CCE_REDUCTION_MEAN,
-                         fake, fake, None, fake, fake, 1 << 30, None)
+                         _lib.CCE_LSE_ALL_ROWS, fake, fake, None, fake, fake, 1 << 30, None)
     assert rc == _lib.CCE_ERR_INVALID_ARG and "smoothing_form" in lib.cce_last_error().decode()
     rc = lib.cce_logits_forward(fake, 0, 1000, fake, 1, 64, 1000, -100, 0.1, 0.0, 5, 1, fake, fake, fake, fake,
                                 1 << 30, None)
@@ -165,7 +186,7 @@ def test_backward_rejects_bad_dtype_and_bias(lib):
 
 
 def test_misaligned_pointers_rejected(lib):
-    rc = lib.cce_forward(0x10002, 0x10000, 0x10000, 1, None, 64, 64, 1000, -100, 0.0, 0.0, 0, 1,
+    rc = lib.cce_forward(0x10002, 0x10000, 0x10000, 1, None, 64, 64, 1000, -100, 0.0, 0.0, 0, 1, 0,
                          0x10000, 0x10000, None, 0x10000, 0x10000, 1 << 20, None)
     assert rc == _lib.CCE_ERR_INVALID_ARG and "aligned" in lib.cce_last_error().decode()
 

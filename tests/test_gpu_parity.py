@@ -160,6 +160,33 @@ def test_labelled_rows_at_the_end(gpu):
     compare(run_hip(gpu, h, w, lab, chunk=512), run_oracle(h, w, lab, chunk=512), "tail rows")
 
 
+@pytest.mark.parametrize("d", [128, 72])
+def test_forward_lse_labelled_rows(gpu, d):
+    """CCE_LSE_LABELLED_ROWS: the same loss and n_valid as CCE_LSE_ALL_ROWS, the
+    same lse / target on labelled rows, 0 on ignored rows (d = 128 compacts
+    the rows; d = 72 runs the register-staged GEMM over every row)."""
+    from chronicals_amd import _lib
+    print(f"case lse_rows d={d}", flush=True)
+    h, w, lab, b = _rand_case(1100, d, 3000, seed=29, ignore_frac=0.0, bias=True)
+    g = torch.Generator().manual_seed(8)
+    lab[torch.randperm(1100, generator=g)[:650]] = IGNORE
+    hd, wd, ld, bd = h.to(gpu, torch.bfloat16), w.to(gpu, torch.bfloat16), lab.to(gpu), b.to(gpu)
+    for red in (_lib.CCE_REDUCTION_MEAN, _lib.CCE_REDUCTION_NONE):
+        out = {}
+        for rows in (_lib.CCE_LSE_ALL_ROWS, _lib.CCE_LSE_LABELLED_ROWS):
+            out[rows] = [t.cpu() for t in torch.ops.chronicals_hip.cce_fwd(hd, wd, ld, bd, IGNORE, 0.1, 1e-3, 0,
+                                                                             red, rows)]
+        (l0, s0, n0, t0), (l1, s1, n1, t1) = out[0], out[1]
+        valid = lab != IGNORE
+        assert int(n0) == int(n1) == int(valid.sum())
+        assert_loss_close(l1.numpy(), l0.numpy(), "loss", rtol=1e-5)
+        np.testing.assert_allclose(s1[valid].numpy(), s0[valid].numpy(), rtol=1e-6, atol=1e-6)
+        np.testing.assert_allclose(t1[valid].numpy(), t0[valid].numpy(), rtol=1e-6, atol=1e-6)
+        assert not s1[~valid].any() and not t1[~valid].any()
+    # the autograd path runs on the labelled-rows forward: against the oracle
+    compare(run_hip(gpu, h, w, lab, b, chunk=1024), run_oracle(h, w, lab, b, chunk=1024), f"lse_rows d={d}")
+
+
 def test_empty_batch(gpu):
     h = torch.zeros(0, 64)
     w = torch.randn(300, 64) * 0.02
