@@ -203,8 +203,9 @@ def main() -> int:
     w = w.to(torch.bfloat16).requires_grad_(not args.frozen_weight)
     N, d, V = cfg.N, cfg.d, cfg.V
     credited_step = (4.0 if args.frozen_weight else 6.0) * N * V * d
-    # the backward skips ignored rows (the forward still computes every row's
-    # log-sum-exp): the figure over labelled rows only is reported beside
+    # forward and backward skip the row tiles past the labelled rows (the
+    # autograd path needs no lse of an ignored row): the figure over labelled
+    # rows only is reported beside
     n_valid = int((lab != -100).sum())
     credited_valid = (4.0 if args.frozen_weight else 6.0) * n_valid * V * d
 
@@ -304,7 +305,7 @@ def main() -> int:
                                f"({kd['credited_gflop_per_launch']:.1f} GFLOP) over its HIP-event average launch "
                                f"time ({kd['avg_launch_us']:.1f} us, {kd['launches_per_step']:g} launches/step); "
                                f"executed incl. recompute {kd['tflops_executed']:.0f} TFLOP/s; both count all N "
-                               f"rows; the backward GEMMs run only the row tiles holding the {n_valid} labelled rows"},
+                               f"rows; the GEMMs run only the row tiles holding the {n_valid} labelled rows"},
         "kernels": kernels,
         "peak_extra_mem_bytes": int(peak_extra),
         "loss": float(loss.item()),
