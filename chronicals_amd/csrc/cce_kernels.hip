@@ -1686,42 +1686,71 @@ __global__ __launch_bounds__(kFusedThreads) void ce_logits_fused_kernel(
   }
 }
 
-// Row compaction of the backward.  One workgroup partitions the rows: the
-// rows whose label is not ignore_index go first, in order (idx[0 .. cnt)),
-// the ignored ones after them (idx[cnt .. N), in reverse order).  live[0] =
-// min(N, 256 * max(1, ceil(cnt / 256))): the row tiles the backward GEMMs run
-// over; the ignored rows inside them carry zero coefficients.
+// Row compaction (forward with labelled rows only, and backward).  One
+// workgroup partitions the rows: the rows whose label is not ignore_index go
+// first, in order (idx[0 .. cnt)), the ignored ones after them (idx[cnt ..
+// N), in reverse order).  live[0] = min(N, 256 * max(1, ceil(cnt / 256))):
+// the row tiles the GEMMs run over; the ignored rows inside them carry zero
+// coefficients (backward) or are not read back (forward).
 __global__ __launch_bounds__(1024) void compact_rows_kernel(const void* labels, int labels64, int N,
                                                             long ignore_index, int* __restrict__ idx,
                                                             int* __restrict__ live) {
-  __shared__ int wsum[2][16];
+  // Rounds of 16384 rows; thread t owns the 16 consecutive rows t*16 ..
+  // t*16+15 of a round, packs their valid bits into a mask, and one
+  // block-wide exclusive scan of the per-thread counts places them.
+  constexpr int kE = 16, kRound = 1024 * kE;
+  __shared__ int wv[16], wi[16];
   __shared__ int base[2];
   const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
   if (tid == 0) base[0] = base[1] = 0;
-  __syncthreads();
-  const uint64_t below = (l == 0) ? 0ull : (~0ull >> (64 - l));
-  for (int r0 = 0; r0 < N; r0 += 1024) {
-    const int n = r0 + tid;
-    const bool in = n < N;
-    const bool valid = in && load_label(labels, labels64, n) != ignore_index;
-    const uint64_t mv = __ballot(valid), mi = __ballot(in && !valid);
-    if (l == 0) {
-      wsum[0][w] = __popcll(mv);
-      wsum[1][w] = __popcll(mi);
+  for (int r0 = 0; r0 < N; r0 += kRound) {
+    const int n0 = r0 + tid * kE;
+    // all 16 loads issued before any is used (indices clamped into range)
+    long lab[kE];
+#pragma unroll
+    for (int k = 0; k < kE; ++k) lab[k] = load_label(labels, labels64, min(n0 + k, N - 1));
+    unsigned mask = 0, inr = 0;
+#pragma unroll
+    for (int k = 0; k < kE; ++k) {
+      if (n0 + k < N) {
+        inr |= 1u << k;
+        if (lab[k] != ignore_index) mask |= 1u << k;
+      }
+    }
+    const int cv = __popc(mask), ci = __popc(inr & ~mask);
+    // inclusive scan of (cv, ci) within the wave
+    int sv = cv, si = ci;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int tv = __shfl_up(sv, o), ti = __shfl_up(si, o);
+      if (l >= o) {
+        sv += tv;
+        si += ti;
+      }
+    }
+    if (l == 63) {
+      wv[w] = sv;
+      wi[w] = si;
     }
     __syncthreads();
-    int ov = base[0], oi = base[1];
+    int ov = base[0] + sv - cv, oi = base[1] + si - ci;  // exclusive offsets within the round
     for (int k = 0; k < w; ++k) {
-      ov += wsum[0][k];
-      oi += wsum[1][k];
+      ov += wv[k];
+      oi += wi[k];
     }
-    if (valid) idx[ov + __popcll(mv & below)] = n;
-    else if (in) idx[N - 1 - (oi + __popcll(mi & below))] = n;
+#pragma unroll
+    for (int k = 0; k < kE; ++k) {
+      if (!((inr >> k) & 1u)) continue;
+      if ((mask >> k) & 1u)
+        idx[ov++] = n0 + k;
+      else
+        idx[N - 1 - oi++] = n0 + k;
+    }
     __syncthreads();
     if (tid == 0) {
       for (int k = 0; k < 16; ++k) {
-        base[0] += wsum[0][k];
-        base[1] += wsum[1][k];
+        base[0] += wv[k];
+        base[1] += wi[k];
       }
     }
     __syncthreads();
