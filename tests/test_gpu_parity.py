@@ -307,6 +307,8 @@ def test_custom_ops_opcheck(gpu):
     for red in (0, 1, 2):
         torch.library.opcheck(torch.ops.chronicals_hip.cce_fwd.default, (hd, wd, ld, bd, IGNORE, 0.1, 1e-4, red % 2, red),
                               test_utils=checks)
+        torch.library.opcheck(torch.ops.chronicals_hip.cce_fwd.default,
+                              (hd, wd, ld, bd, IGNORE, 0.1, 1e-4, red % 2, red, 1), test_utils=checks)
     loss, lse, nv, _ = torch.ops.chronicals_hip.cce_fwd(hd, wd, ld, bd, IGNORE, 0.0, 0.0, 0, 1)
     g = torch.tensor(1.0, device=gpu)
     for need in ((True, True, True), (False, True, False), (True, False, True)):
