@@ -187,6 +187,30 @@ def test_forward_lse_labelled_rows(gpu, d):
     compare(run_hip(gpu, h, w, lab, b, chunk=1024), run_oracle(h, w, lab, b, chunk=1024), f"lse_rows d={d}")
 
 
+def test_forward_labelled_rows_resplits_vocabulary(gpu):
+    """Many row tiles, half the rows ignored: the compacted forward re-splits
+    the vocabulary over its live row tiles on the device (64 splits per tile
+    here, against 32 on the host) and must give the all-rows forward's lse."""
+    from chronicals_amd import _lib
+    N, d, V = 65536, 64, 20000
+    g = torch.Generator().manual_seed(31)
+    h = (torch.randn(N, d, generator=g)).to(gpu, torch.bfloat16)
+    w = (torch.randn(V, d, generator=g) * 0.2).to(gpu, torch.bfloat16)
+    lab = torch.randint(0, V, (N,), generator=g)
+    lab[torch.rand(N, generator=g) < 0.5] = IGNORE
+    ld = lab.to(gpu)
+    out = {}
+    for rows in (_lib.CCE_LSE_ALL_ROWS, _lib.CCE_LSE_LABELLED_ROWS):
+        out[rows] = [t.cpu() for t in torch.ops.chronicals_hip.cce_fwd(h, w, ld, None, IGNORE, 0.0, 0.0, 0,
+                                                                         _lib.CCE_REDUCTION_MEAN, rows)]
+    (l0, s0, n0, _), (l1, s1, n1, _) = out[0], out[1]
+    valid = lab != IGNORE
+    assert int(n0) == int(n1) == int(valid.sum())
+    assert_loss_close(float(l1), float(l0), "loss", rtol=1e-5)
+    np.testing.assert_allclose(s1[valid].numpy(), s0[valid].numpy(), rtol=1e-6, atol=1e-6)
+    assert not s1[~valid].any()
+
+
 def test_empty_batch(gpu):
     h = torch.zeros(0, 64)
     w = torch.randn(300, 64) * 0.02
