@@ -759,19 +759,37 @@ struct EpiAcc {
   static __device__ inline void tile(const Params& p, State&, WaveAcc<BN, W>& acc, const GemmShape& g, int tm,
                                      int tn, int wm, int wn, int l, bf16_t*) {
     constexpr int FN = BN / 64;
+    constexpr int JG = FN >= 2 ? 2 : 1;  // 32 x 64 column blocks whose old values load together
     pin_epilogue(l, tm, tn);
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int m = tm * kBM + acc_row<W>(wm, i, l);
       if (m >= g.M) continue;
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
+      for (int j0 = 0; j0 < FN; j0 += JG) {
+        // the accumulator's old values for JG column blocks, all loads issued
+        // before any add or store (one memory round trip per group, not per
+        // 16-byte piece)
+        f32x4 old[JG][4];
+        if (p.mode >= 2) {
+#pragma unroll
+          for (int jj = 0; jj < JG; ++jj)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int n = tn * BN + acc_col<BN>(wn, j0 + jj, q, l);
+              old[jj][q] = n < g.N ? *reinterpret_cast<const f32x4*>(p.acc32 + (long)m * p.ldacc + n)
+                                   : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+#pragma unroll
+        for (int jj = 0; jj < JG; ++jj)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
+          const int j = j0 + jj;
           const int n = tn * BN + acc_col<BN>(wn, j, q, l);
           if (n >= g.N) continue;
           f32x4 v = {acc.v[i][j][4 * q], acc.v[i][j][4 * q + 1], acc.v[i][j][4 * q + 2], acc.v[i][j][4 * q + 3]};
-          if (p.mode >= 2) v += *reinterpret_cast<const f32x4*>(p.acc32 + (long)m * p.ldacc + n);
+          if (p.mode >= 2) v += old[jj][q];
           if (p.mode == 1 || p.mode == 2) {
             *reinterpret_cast<f32x4*>(p.acc32 + (long)m * p.ldacc + n) = v;
           } else {
@@ -784,6 +802,7 @@ struct EpiAcc {
             }
           }
         }
+      }
     }
   }
   static __device__ inline void finish(const Params&, State&, const GemmShape&, int, int, bf16_t*, int, int,
