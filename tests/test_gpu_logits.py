@@ -214,6 +214,43 @@ def test_deterministic():
     assert torch.equal(outs[0][1], outs[1][1])
 
 
+def test_side_streams_concurrent_no_host_sync():
+    """The logits-in ops launch on the caller's current stream and never
+    synchronise with the host: two problems run concurrently on two side
+    streams under torch's sync debug mode "error", each after a bounded spin
+    and a fresh input copy on its own stream, and match the default-stream
+    results bitwise."""
+    m = _mod()
+    cases = [_case(300, 50257, torch.bfloat16, seed=43), _case(700, 32000, torch.float32, seed=44)]
+    refs = []
+    for x, lab in cases:
+        xr = x.to(DEV).requires_grad_(True)
+        loss = m.chunked_cross_entropy_loss(xr, lab.to(DEV), label_smoothing=0.1, z_loss_weight=1e-4)
+        loss.backward()
+        torch.cuda.synchronize()
+        refs.append((loss.detach().clone(), xr.grad.clone()))
+    sources = [(x.to(DEV), lab.to(DEV)) for x, lab in cases]
+    main = torch.cuda.current_stream()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = []
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        for s, (x0, l0) in zip(streams, sources):
+            s.wait_stream(main)
+            with torch.cuda.stream(s):
+                torch.cuda._sleep(20_000_000)  # about 10 ms of spinning on this stream
+                xr = x0.clone().requires_grad_(True)
+                loss = m.chunked_cross_entropy_loss(xr, l0.clone(), label_smoothing=0.1, z_loss_weight=1e-4)
+                loss.backward()
+                outs.append((loss, xr))
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    torch.cuda.synchronize()
+    for i, ((rl, rg), (loss, xr)) in enumerate(zip(refs, outs)):
+        assert torch.equal(loss.detach(), rl), f"case {i} loss"
+        assert torch.equal(xr.grad, rg), f"case {i} grad"
+
+
 def test_full_size_C2_logits_against_gpu_closed_form():
     # N x V of C2 (16384 x 151936 bf16 logits, 5 GB): float64-accumulated closed form on the GPU, by row blocks
     m = _mod()

@@ -297,6 +297,49 @@ def test_deterministic(gpu):
         assert np.array_equal(a[k], c[k]), k
 
 
+def test_side_streams_concurrent_no_host_sync(gpu):
+    """The ops launch on the caller's current stream, keep no state between
+    calls and never synchronise with the host: two problems, forward and
+    backward, are issued on two side streams (default priority) under torch's
+    sync debug mode "error" (a synchronising torch call raises), then compared
+    bitwise with the same problems run one after the other on the default
+    stream.  Each side stream first spins for a bounded time and only then
+    makes the input copies the op reads, so a launch on any other stream
+    would read them before they are written."""
+    cases = [_rand_case(700, 128, 4000, seed=21, bias=True), _rand_case(1300, 256, 9000, seed=22)]
+    refs = [run_hip(gpu, h, w, lab, b, chunk=2048) for h, w, lab, b in cases]
+    sources = []
+    for h, w, lab, b in cases:
+        sources.append((h.to(gpu, torch.bfloat16), w.to(gpu, torch.bfloat16), lab.to(gpu),
+                        None if b is None else b.to(gpu, torch.float32)))
+    main = torch.cuda.current_stream(gpu)
+    streams = [torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)]
+    prepared, losses = [], []
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        for s, (h0, w0, l0, b0) in zip(streams, sources):
+            s.wait_stream(main)
+            with torch.cuda.stream(s):
+                torch.cuda._sleep(20_000_000)  # about 10 ms of spinning on this stream
+                hd = h0.clone().requires_grad_(True)
+                wd = w0.clone().requires_grad_(True)
+                bd = None if b0 is None else b0.clone().requires_grad_(True)
+                ld = l0.clone()
+                loss = _cce()(hd, wd, ld, bd, 2048, IGNORE, 0.0, 0.0)
+                loss.backward()
+                prepared.append((hd, wd, ld, bd))
+                losses.append(loss)
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    torch.cuda.synchronize()
+    for i, (ref, (hd, wd, ld, bd), loss) in enumerate(zip(refs, prepared, losses)):
+        assert np.array_equal(loss.detach().float().cpu().numpy(), ref["loss"]), f"case {i} loss"
+        assert np.array_equal(hd.grad.float().cpu().numpy(), ref["dh"]), f"case {i} dh"
+        assert np.array_equal(wd.grad.float().cpu().numpy(), ref["dw"]), f"case {i} dw"
+        if bd is not None:
+            assert np.array_equal(bd.grad.float().cpu().numpy(), ref["db"]), f"case {i} db"
+
+
 @pytest.mark.parametrize("name", ["C2", "C3", "C4", "C5"])
 def test_full_size_vs_torch_fp32(gpu, name):
     """Every benchmark configuration at full size against an fp32 torch
