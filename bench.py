@@ -10,8 +10,10 @@ among launches that carry algorithmic work: the forward GEMM, and the per-band
 launch holding the dHidden / dWeight GEMMs — with the next band's logits
 recompute, which is executed but not credited, as the algorithmic work of a
 fwd+bwd step is 6*N*V*d FLOPs) is timed with HIP events on its own launch
-stream by the library (cce_kernel_timing_enable) over the timed region; the
-library reports each launch's credited and executed FLOPs.
+stream by the library (cce_kernel_timing_enable) over K further steps after the
+K timed steps; the library reports each launch's credited and executed FLOPs.
+The timed steps carry no per-launch events (one event between steps only):
+events between a step's kernels add about 0.5% to a C2 step.
 
 ``--workload logits`` measures the logits-in cross-entropy instead
 (chunked_cross_entropy_loss over [N, V] bf16 logits of the same C2 shape,
@@ -37,6 +39,44 @@ PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 4096 FLOP/clk x 2.4 GHz (dense bf16 MFMA)
 PEAK_HBM_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 TRAFFIC_LOGITS_FILE = os.path.join(REPO, "profiles", "traffic_logits.json")
+
+
+def timed_steps(step, steps: int):
+    """Mean ms per step over `steps` steps, the sorted per-step times and the
+    last step's result.  One event on the current stream between consecutive
+    steps; nothing is recorded between the kernels of a step."""
+    import torch
+
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    out = None
+    torch.cuda.synchronize()
+    evs[0].record()
+    for i in range(steps):
+        out = step()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    return (evs[0].elapsed_time(evs[-1]) / steps, sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(steps)),
+            out)
+
+
+def kernel_timed_steps(step, steps: int) -> None:
+    """`steps` further steps with the library's per-launch HIP events on each
+    launch's stream (read back with kernel_timing_read).  The events sit
+    between kernels and add about 0.5% to a C2 step, so the headline step
+    time is measured without them."""
+    import torch
+    from chronicals_amd import _lib
+
+    torch.cuda.synchronize()
+    for k in range(_lib.CCE_KERNEL_KINDS):
+        _lib.kernel_timing_read(k)  # drop anything recorded so far
+    _lib.kernel_timing_enable(True)
+    try:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    finally:
+        _lib.kernel_timing_enable(False)
 
 
 def cpu_model() -> str:
@@ -219,31 +259,20 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    for k in range(_lib.CCE_KERNEL_KINDS):
-        _lib.kernel_timing_read(k)  # drop anything recorded so far
     base_mem = torch.cuda.memory_allocated()
     torch.cuda.reset_peak_memory_stats()
-    # one event between consecutive steps: the mean over the K steps is the
-    # headline, the per-step spread is reported beside it
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    _lib.kernel_timing_enable(True)
-    torch.cuda.synchronize()
-    evs[0].record()
-    for i in range(args.steps):
-        loss = step()
-        evs[i + 1].record()
-    torch.cuda.synchronize()
-    _lib.kernel_timing_enable(False)
-    ms = evs[0].elapsed_time(evs[-1]) / args.steps
-    step_ms = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps))
+    # the mean over the K timed steps is the headline, the per-step spread is
+    # reported beside it
+    ms, step_ms, loss = timed_steps(step, args.steps)
 
     def pct(q):
         return step_ms[min(len(step_ms) - 1, int(round(q * (len(step_ms) - 1))))]
     peak_extra = torch.cuda.max_memory_allocated() - base_mem
 
-    # per-kernel breakdown with the library's own FLOP accounting per launch:
-    # credited = algorithmic (forward logits, dHidden, dWeight), executed adds
-    # the backward's logits recompute
+    # per-kernel breakdown over K further steps, with the library's own FLOP
+    # accounting per launch: credited = algorithmic (forward logits, dHidden,
+    # dWeight), executed adds the backward's logits recompute
+    kernel_timed_steps(step, args.steps)
     kernels = {}
     for k, name in _lib.KERNEL_KIND_NAMES.items():
         tot_ms, n, cr, ex = _lib.kernel_timing_read(k)
@@ -349,23 +378,12 @@ def bench_logits(args) -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    for k in range(_lib.CCE_KERNEL_KINDS):
-        _lib.kernel_timing_read(k)
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    _lib.kernel_timing_enable(True)
-    torch.cuda.synchronize()
-    evs[0].record()
-    for i in range(args.steps):
-        loss = step()
-        evs[i + 1].record()
-    torch.cuda.synchronize()
-    _lib.kernel_timing_enable(False)
-    ms = evs[0].elapsed_time(evs[-1]) / args.steps
-    step_ms = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps))
+    ms, step_ms, loss = timed_steps(step, args.steps)
 
     def pct(q):
         return step_ms[min(len(step_ms) - 1, int(round(q * (len(step_ms) - 1))))]
 
+    kernel_timed_steps(step, args.steps)
     kernels = {}
     for k in (_lib.CCE_KERNEL_LOGITS_FWD, _lib.CCE_KERNEL_LOGITS_BWD, _lib.CCE_KERNEL_LOGITS_FUSED):
         tot_ms, n, by, _ = _lib.kernel_timing_read(k)
