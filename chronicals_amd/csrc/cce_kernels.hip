@@ -53,8 +53,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // Per-GEMM configuration: wave layout W (8 or 4), column tile BN and main-loop
 // pipeline PIPE (4: direct-to-LDS loads, needs K-major operands with K a
-// multiple of 64; 3: register-staged loads, any K; 1: simple register
-// pipeline).  The "fallback" configuration serves K % 64 != 0.
+// multiple of 64; 5: as 4 with an MN-major A read back transposed; 3:
+// register-staged loads, any K).  The "fallback" configuration serves
+// K % 64 != 0.
 constexpr int kWarp8 = 8;
 constexpr int kFastBN = 256;    // PIPE 4 kernels
 constexpr int kSlowBN = 128;    // PIPE 3 kernels
@@ -810,10 +811,11 @@ struct EpiAcc {
 };
 
 // ---------------------------------------------------------------------------
-// The GEMM kernel: C[M,N] = A[M,K] . B[N,K]^T, 256 x BN x 64 tiles, two LDS
+// The GEMM kernel: C[M,N] = A[M,K] . B[N,K]^T, 256 x BN x 64 tiles.  PIPE 4 / 5
+// (direct-to-LDS) are described at their loop below.  PIPE 3 has two LDS
 // stages and two register sets of prefetched slabs.
 //
-// Software pipeline (per slab s, LDS stage p = s & 1):
+// PIPE 3 software pipeline (per slab s, LDS stage p = s & 1):
 //   - global loads of slab s+2 go to register set p (issued unconditionally:
 //     past the last slab the loaders' bounds predicates read zeros, so the
 //     compiler's outstanding-load counts stay exact);
@@ -838,6 +840,7 @@ constexpr int gemm_lds_elems(int pipe, int nst = 2) {
 template <int BN, int W, bool AK, bool BKM, template <int, int> class EpiT, int PIPE, int NST = 2>
 __device__ __forceinline__ void gemm_body(const GemmShape& g_in, const typename EpiT<BN, W>::Params& ep, int bid,
                                           int nb, bf16_t* smem) {
+  static_assert(PIPE >= 3 && PIPE <= 5, "pipelines: 3 (register-staged), 4 and 5 (direct-to-LDS)");
   typedef EpiT<BN, W> Epi;
   GemmShape g = g_in;
   if (g.dyn == kDynK) g.K = min(g.K, *g.live);
@@ -993,49 +996,6 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g_in, const typename 
     return;
   }
 
-  if constexpr (PIPE == 1) {
-    // Simple pipeline: one slab in flight in registers, fragments read per
-    // k-step.  Its smaller register footprint suits 256-column tiles with 8
-    // waves, whose epilogue needs the room.
-    typename LoaderSel<AK, kBM, W>::type la;
-    typename LoaderSel<BKM, BN, W>::type lb;
-    la.load(g.A, g.lda, a_r0, g.M, 0, g.K, tid);
-    lb.load(g.B, g.ldb, t0 * BN, g.N, 0, g.K, tid);
-    la.store(S0, tid);
-    lb.store(S0 + kBM * kPitch, tid);
-    __syncthreads();
-    int s = 0;
-    for (int tn = t0; tn < t1; ++tn) {
-      acc.zero();
-      for (int kt = 0; kt < KT; ++kt, ++s) {
-        bf16_t* const Sc = (s & 1) ? S1 : S0;
-        bf16_t* const Sn = (s & 1) ? S0 : S1;
-        const bool last_k = (kt + 1 == KT);
-        const bool more = !(last_k && tn + 1 == t1);
-        if (more) {
-          const int nt = last_k ? tn + 1 : tn;
-          const int nk = last_k ? 0 : kt + 1;
-          la.load(g.A, g.lda, a_r0, g.M, nk * kBK, g.K, tid);
-          lb.load(g.B, g.ldb, nt * BN, g.N, nk * kBK, g.K, tid);
-        }
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          Frags<BN, W> f;
-          read_frags<BN, W>(Sc, Sc + kBM * kPitch, kk, f, wm, wn, l);
-          mfma_frags<BN, W>(f, acc);
-        }
-        if (more) {
-          la.store(Sn, tid);
-          lb.store(Sn + kBM * kPitch, tid);
-        }
-        __syncthreads();
-      }
-      Epi::tile(ep, st, acc, g, tm, tn, wm, wn, l, scratch);
-    }
-    Epi::finish(ep, st, g, tm, split, smem, wm, wn, l);
-    return;
-  }
-
   typename LoaderSel<AK, kBM, W>::type la0, la1;
   typename LoaderSel<BKM, BN, W>::type lb0, lb1;
   Frags<BN, W> f0, f1;
@@ -1054,11 +1014,6 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g_in, const typename 
     if constexpr (decltype(LOAD)::value) {
       la.load(g.A, g.lda, a_r0, g.M, nk * kBK, g.K, tid);
       lb.load(g.B, g.ldb, nt * BN, g.N, nk * kBK, g.K, tid);
-#ifdef CCE_PIN_LOADS
-      // keep the slab s+2 loads at the top of the slab: the scheduler would
-      // otherwise sink them below the LDS drain and halve the prefetch distance
-      __builtin_amdgcn_sched_barrier(0);
-#endif
     }
     read_frags<BN, W>(Sc, Sc + kBM * kPitch, 1, f1, wm, wn, l);
     mfma_frags<BN, W>(f0, acc);
