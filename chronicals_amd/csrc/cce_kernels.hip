@@ -2443,9 +2443,14 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
 
   const long nbands = ceil_div(V, Vb);
   const int gm = (int)ceil_div(N, kBM);
+  // The partial band (V - (nbands - 1) * Vb columns) comes first: its logits
+  // recompute then runs alone, where it is shortest, and the last launch,
+  // which has no next band's recompute to fill the CUs its long dW tiles
+  // leave idle, gets a full band.
+  const long head = V - (nbands - 1) * Vb;
   auto band_cols = [&](long b, long& v0, long& vb, long& vb64) {
-    v0 = b * Vb;
-    vb = (V - v0 < Vb) ? (V - v0) : Vb;
+    v0 = b == 0 ? 0 : head + (b - 1) * Vb;
+    vb = b == 0 ? head : Vb;
     vb64 = (long)align_up((size_t)vb, 64);
   };
   // dH of one band: G[N][vb64] . WT[d][vb64]^T over hidden columns [c0, c0 + nc)
