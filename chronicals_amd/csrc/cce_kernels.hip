@@ -1120,7 +1120,29 @@ struct BandLaunch {
   GradParams e_gr;
   TransposeParams tr;
   int nb_dw, nb_dw2, nb_dh, nb_dh2, nb_gr, nb_tr;
+  // dH split over the band's K (few row tiles): with dh_ks > 1 each dH tile
+  // has dh_ks workgroups; split k covers K columns [k*dh_kc, (k+1)*dh_kc) and
+  // writes its fp32 partial with e_dh*_part (mode 1) into slice k of the
+  // partial buffer (dh_part_stride floats apart), which dh_reduce_kernel
+  // folds into the accumulator after the launch.
+  int dh_ks, dh_kc;
+  long dh_part_stride;
+  AccParams e_dh_part, e_dh2_part;
 };
+
+// One split workgroup of a K-split dH population (see BandLaunch).
+template <int BN, int NST>
+__device__ inline void dh_split_body(const GemmShape& g0, const AccParams& e0, int ks, int kc, long stride, int b,
+                                     int nb, bf16_t* smem) {
+  const int k = b % ks, k0 = k * kc;
+  GemmShape g = g0;
+  AccParams e = e0;
+  g.A += k0;
+  g.B += k0;
+  g.K = min(kc, g0.K - k0);
+  e.acc32 += k * stride;
+  gemm_body<BN, kWarp8, true, true, EpiAcc, 4, NST>(g, e, b / ks, nb / ks, smem);
+}
 
 template <int NT>
 __device__ inline void transpose_tile(const bf16_t* __restrict__ in, long ldi, int R, int C, bf16_t* __restrict__ out,
@@ -1141,12 +1163,18 @@ __global__ __launch_bounds__(kWarp8 * 64) void band_kernel(BandLaunch p) {
   }
   b -= p.nb_dw2;
   if (b < p.nb_dh) {
-    gemm_body<kFastBN, kWarp8, true, true, EpiAcc, 4>(p.dh, p.e_dh, b, p.nb_dh, smem);
+    if (p.dh_ks > 1)
+      dh_split_body<kFastBN, 2>(p.dh, p.e_dh_part, p.dh_ks, p.dh_kc, p.dh_part_stride, b, p.nb_dh, smem);
+    else
+      gemm_body<kFastBN, kWarp8, true, true, EpiAcc, 4>(p.dh, p.e_dh, b, p.nb_dh, smem);
     return;
   }
   b -= p.nb_dh;
   if (b < p.nb_dh2) {
-    gemm_body<kSlowBN, kWarp8, true, true, EpiAcc, 4, 3>(p.dh2, p.e_dh2, b, p.nb_dh2, smem);
+    if (p.dh_ks > 1)
+      dh_split_body<kSlowBN, 3>(p.dh2, p.e_dh2_part, p.dh_ks, p.dh_kc, p.dh_part_stride, b, p.nb_dh2, smem);
+    else
+      gemm_body<kSlowBN, kWarp8, true, true, EpiAcc, 4, 3>(p.dh2, p.e_dh2, b, p.nb_dh2, smem);
     return;
   }
   b -= p.nb_dh2;
@@ -1764,6 +1792,38 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(char* __restrict__ out, 
   }
 }
 
+// dH of one band split over the band's K (few row tiles): the ks fp32
+// partials P[k] = P + k * stride ([rows][d], GEMM row order) of each live row
+// are summed in fixed order and applied with the band's accumulator mode, as
+// the GEMM epilogue applies an unsplit tile: 0 out = s, 1 acc = s,
+// 2 acc += s, 3 out = acc + s; out rows go through the row map.  d % 64 == 0.
+__global__ __launch_bounds__(256) void dh_reduce_kernel(const float* __restrict__ P, long stride, int ks, int N,
+                                                        int d, const int* __restrict__ live, float* __restrict__ acc,
+                                                        int mode, void* __restrict__ out, int out_f32,
+                                                        const int* __restrict__ rowmap) {
+  const int rows = live ? min(live[0], N) : N;
+  const int q = d >> 2;
+  const long total = (long)rows * q;
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
+    const int m = (int)(i / q);
+    const long o = (long)m * d + (i % q) * 4;
+    f32x4 s = *reinterpret_cast<const f32x4*>(P + o);
+    for (int k = 1; k < ks; ++k) s += *reinterpret_cast<const f32x4*>(P + k * stride + o);
+    if (mode == 1 || mode == 2) {
+      if (mode == 2) s = *reinterpret_cast<const f32x4*>(acc + o) + s;
+      *reinterpret_cast<f32x4*>(acc + o) = s;
+      continue;
+    }
+    if (mode == 3) s = *reinterpret_cast<const f32x4*>(acc + o) + s;
+    const long oo = (long)(rowmap ? rowmap[m] : m) * d + (i % q) * 4;
+    if (out_f32)
+      *reinterpret_cast<f32x4*>(static_cast<float*>(out) + oo) = s;
+    else
+      *reinterpret_cast<u32x2*>(static_cast<bf16_t*>(out) + oo) = u32x2{pack_bf16x2(s[0], s[1]),
+                                                                         pack_bf16x2(s[2], s[3])};
+  }
+}
+
 // Per-row backward coefficients, for GEMM row i of source row idx[i] (idx
 // null: i).
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__ grad_out,
@@ -2026,12 +2086,33 @@ struct BwdLayout {
   int* idx;
   int* live;
   bf16_t* Hc;
+  // fp32 partials of a K-split dH (dh_ks slices of [N][d]); null when unsplit
+  float* dhpart;
+  int dh_ks;
   size_t bytes;
 };
 
 // The banded backward with the band kernel (d a multiple of 64) overlaps the
 // recompute of band b+1 with the dW / dH GEMMs of band b: two G buffers.
 bool banded(long d) { return d % 64 == 0; }
+
+// Hidden columns of the banded backward's 256-wide dW / dH tiles; the rest,
+// when d % 256 <= 128, is one 128-wide tail tile.
+long band_dmain(long d) { return (d % 256 == 0 || d % 256 > 128) ? d : d - d % 256; }
+
+// K splits of the banded dH.  dH has one tile per (256-row tile, hidden
+// column tile), each reducing over the whole band; with few rows those tiles
+// cannot fill the CUs and the band launch waits on their long K loops.  Then
+// K is split so that tiles x splits reaches about 256 workgroups, with at
+// least 8 slabs of 64 per split.
+int dh_splits(long N, long d, long Vb) {
+  if (!banded(d) || N <= 0 || d <= 0) return 1;
+  const long dmain = band_dmain(d);
+  const long tiles = ceil_div(N, kBM) * (ceil_div(dmain, kFastBN) + (dmain < d ? 1 : 0));
+  if (tiles <= 0 || tiles >= 128) return 1;
+  const long ks = std::min<long>(ceil_div(256, tiles), Vb / 512);
+  return ks < 2 ? 1 : (int)ks;
+}
 
 BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bool need_dw) {
   Carver c(ws);
@@ -2050,6 +2131,8 @@ BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bo
   L.idx = compact ? c.take<int>((size_t)N) : nullptr;
   L.live = compact ? c.take<int>(1) : nullptr;
   L.Hc = compact ? c.take<bf16_t>((size_t)N * d) : nullptr;
+  L.dh_ks = need_dh ? dh_splits(N, d, Vb) : 1;
+  L.dhpart = L.dh_ks > 1 ? c.take<float>((size_t)L.dh_ks * N * d) : nullptr;
   L.bytes = align_up(c.off, 256);
   return L;
 }
@@ -2516,7 +2599,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
   if (banded(d)) {
     // launch b: dW(b), dH(b) from G[b & 1] and the recompute of band b+1 into
     // G[(b+1) & 1]; band 0's recompute runs alone first.
-    const long dmain = (d % 256 == 0 || d % 256 > 128) ? d : d - d % 256;
+    const long dmain = band_dmain(d);
     {
       long v0, vb, vb64;
       band_cols(0, v0, vb, vb64);
@@ -2547,13 +2630,28 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       }
       if (need_dh) {
         if (b + 1 < nbands) p.nb_tr = transpose_params(b + 1, p.tr);  // into the other WT buffer
+        // K splits of this band: every split non-empty and a whole number of slabs
+        int ks = 1;
+        if (L.dhpart) {
+          long v0, vb, vb64;
+          band_cols(b, v0, vb, vb64);
+          p.dh_kc = (int)align_up((size_t)ceil_div(vb64, L.dh_ks), 64);
+          ks = (int)ceil_div(vb64, p.dh_kc);
+        }
+        p.dh_ks = ks;
+        p.dh_part_stride = N * d;
         if (dmain > 0) {
           dh_shape(b, G, 0, dmain, p.dh, p.e_dh);
-          p.nb_dh = gm * (int)ceil_div(dmain, kFastBN);
+          p.nb_dh = gm * (int)ceil_div(dmain, kFastBN) * ks;
+          p.e_dh_part = p.e_dh;
+          p.e_dh_part.acc32 = L.dhpart; p.e_dh_part.ldacc = d; p.e_dh_part.mode = 1; p.e_dh_part.rowmap = nullptr;
         }
         if (dmain < d) {
           dh_shape(b, G, dmain, d - dmain, p.dh2, p.e_dh2);
-          p.nb_dh2 = gm * (int)ceil_div(d - dmain, kSlowBN);
+          p.nb_dh2 = gm * (int)ceil_div(d - dmain, kSlowBN) * ks;
+          p.e_dh2_part = p.e_dh2;
+          p.e_dh2_part.acc32 = L.dhpart ? L.dhpart + dmain : nullptr; p.e_dh2_part.ldacc = d;
+          p.e_dh2_part.mode = 1; p.e_dh2_part.rowmap = nullptr;
         }
       }
       if (b + 1 < nbands) {
@@ -2563,6 +2661,14 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       }
       rc = launch_band(p, bias != nullptr, st);
       if (rc) return rc;
+      if (need_dh && p.dh_ks > 1) {
+        const AccParams& e = dmain > 0 ? p.e_dh : p.e_dh2;
+        const long total = N * (d / 4);
+        hipLaunchKernelGGL(dh_reduce_kernel, dim3((unsigned)std::min<long>(ceil_div(total, 256), 2048)), dim3(256), 0,
+                           st, L.dhpart, p.dh_part_stride, p.dh_ks, (int)N, (int)d, L.live, L.dHacc, e.mode,
+                           grad_hidden, (int)(grad_hidden_dtype == CCE_DTYPE_F32), L.idx);
+        HIP_TRY(hipGetLastError());
+      }
       if (need_db) {
         rc = colsum_band(b, G);
         if (rc) return rc;

@@ -92,6 +92,28 @@ def test_ragged_shapes(gpu, N, d, V, chunk):
     compare(run_hip(gpu, h, w, lab, chunk=chunk), run_oracle(h, w, lab, chunk=chunk), f"N{N}d{d}V{V}")
 
 
+@pytest.mark.parametrize("N,d,V,chunk,hdtype,reduction,ignore_frac", [
+    # 9 dH tiles: 15-16 K splits; a partial first band and two full ones (accumulator modes 1, 2, 3);
+    # fp32 gradients; per-row grad_output
+    (700, 768, 20000, 8192, torch.float32, "none", 0.1),
+    # d = 256 + 64: the 128-wide tail tile is split too; most rows ignored (one live row tile of three)
+    (600, 320, 9000, 4096, torch.bfloat16, "mean", 0.7),
+    # one band (mode 0: straight to the output; the band is 3072 wide): 6 splits of 512 columns, the last shorter
+    (130, 512, 3000, 8192, torch.bfloat16, "sum", 0.1),
+])
+def test_small_batch_split_dh(gpu, N, d, V, chunk, hdtype, reduction, ignore_frac):
+    """With few 256-row tiles the banded dH splits each band's K over several
+    workgroups (fp32 partials, then a fixed-order reduction that applies the
+    band's accumulator mode); against the oracle, and bitwise repeatable."""
+    print(f"case split dH N={N} d={d} V={V} chunk={chunk} {hdtype} {reduction}", flush=True)
+    h, w, lab, _ = _rand_case(N, d, V, seed=N + d, ignore_frac=ignore_frac)
+    go = torch.rand(N, generator=torch.Generator().manual_seed(4)) if reduction == "none" else None
+    got = run_hip(gpu, h, w, lab, chunk=chunk, reduction=reduction, grad_output=go, hdtype=hdtype)
+    compare(got, run_oracle(h, w, lab, chunk=chunk, reduction=reduction, grad_output=go), f"split N{N}d{d}")
+    again = run_hip(gpu, h, w, lab, chunk=chunk, reduction=reduction, grad_output=go, hdtype=hdtype)
+    assert np.array_equal(got["dh"], again["dh"]) and np.array_equal(got["dw"], again["dw"])
+
+
 @pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
 @pytest.mark.parametrize("bias", [False, True])
 def test_reductions_and_bias(gpu, reduction, bias):
