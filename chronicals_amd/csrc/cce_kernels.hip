@@ -2103,14 +2103,15 @@ long band_dmain(long d) { return (d % 256 == 0 || d % 256 > 128) ? d : d - d % 2
 // K splits of the banded dH.  dH has one tile per (256-row tile, hidden
 // column tile), each reducing over the whole band; with few rows those tiles
 // cannot fill the CUs and the band launch waits on their long K loops.  Then
-// K is split so that tiles x splits reaches about 256 workgroups, with at
-// least 8 slabs of 64 per split.
+// K is split so that tiles x splits reaches about 128 workgroups, with at
+// least 8 slabs of 64 per split (more splits cost more in the fp32 partials'
+// reduction than their shorter K loops return).
 int dh_splits(long N, long d, long Vb) {
   if (!banded(d) || N <= 0 || d <= 0) return 1;
   const long dmain = band_dmain(d);
   const long tiles = ceil_div(N, kBM) * (ceil_div(dmain, kFastBN) + (dmain < d ? 1 : 0));
   if (tiles <= 0 || tiles >= 128) return 1;
-  const long ks = std::min<long>(ceil_div(256, tiles), Vb / 512);
+  const long ks = std::min<long>(ceil_div(128, tiles), Vb / 512);
   return ks < 2 ? 1 : (int)ks;
 }
 

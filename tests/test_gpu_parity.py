@@ -93,7 +93,7 @@ def test_ragged_shapes(gpu, N, d, V, chunk):
 
 
 @pytest.mark.parametrize("N,d,V,chunk,hdtype,reduction,ignore_frac", [
-    # 9 dH tiles: 15-16 K splits; a partial first band and two full ones (accumulator modes 1, 2, 3);
+    # 9 dH tiles: 15 K splits; a partial first band and two full ones (accumulator modes 1, 2, 3);
     # fp32 gradients; per-row grad_output
     (700, 768, 20000, 8192, torch.float32, "none", 0.1),
     # d = 256 + 64: the 128-wide tail tile is split too; most rows ignored (one live row tile of three)
