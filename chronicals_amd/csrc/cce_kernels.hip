@@ -1096,7 +1096,52 @@ __global__ __launch_bounds__(W * 64) void dual_acc_kernel(GemmShape g_dw, AccPar
 // idle at the end of the band.  The 128-wide tail tiles fit three LDS stages
 // (two slabs in flight) in the space the 256-wide tiles use for two.
 // The transpose of the next band's W rows (dH's B operand) rides along as the
-// last, shortest population: one 64 x 64 tile per workgroup.
+// last, shortest population: one 64 x 64 tile per workgroup.  With dH split
+// over K on very few rows, the previous band's partials are reduced by a
+// population placed just before the transposes.
+
+// dH of one band split over the band's K (few row tiles): the ks fp32
+// partials P[k] = P + k * stride ([rows][d], GEMM row order) of each live row
+// are summed in fixed order and applied with the band's accumulator mode, as
+// the GEMM epilogue applies an unsplit tile: 0 out = s, 1 acc = s,
+// 2 acc += s, 3 out = acc + s; out rows go through the row map.  d % 64 == 0.
+struct DhReduce {
+  const float* P;
+  long stride;
+  int ks, N, d;
+  const int* live;
+  float* acc;
+  int mode;
+  void* out;
+  int out_f32;
+  const int* rowmap;
+};
+
+// Items (row, 4 columns) first, first + step, ... of a DhReduce.
+__device__ inline void dh_reduce_body(const DhReduce& r, long first, long step) {
+  const int rows = r.live ? min(r.live[0], r.N) : r.N;
+  const int q = r.d >> 2;
+  const long total = (long)rows * q;
+  for (long i = first; i < total; i += step) {
+    const int m = (int)(i / q);
+    const long o = (long)m * r.d + (i % q) * 4;
+    f32x4 s = *reinterpret_cast<const f32x4*>(r.P + o);
+    for (int k = 1; k < r.ks; ++k) s += *reinterpret_cast<const f32x4*>(r.P + k * r.stride + o);
+    if (r.mode == 1 || r.mode == 2) {
+      if (r.mode == 2) s = *reinterpret_cast<const f32x4*>(r.acc + o) + s;
+      *reinterpret_cast<f32x4*>(r.acc + o) = s;
+      continue;
+    }
+    if (r.mode == 3) s = *reinterpret_cast<const f32x4*>(r.acc + o) + s;
+    const long oo = (long)(r.rowmap ? r.rowmap[m] : m) * r.d + (i % q) * 4;
+    if (r.out_f32)
+      *reinterpret_cast<f32x4*>(static_cast<float*>(r.out) + oo) = s;
+    else
+      *reinterpret_cast<u32x2*>(static_cast<bf16_t*>(r.out) + oo) = u32x2{pack_bf16x2(s[0], s[1]),
+                                                                           pack_bf16x2(s[2], s[3])};
+  }
+}
+
 struct TransposeParams {
   const bf16_t* in;
   long ldi;
@@ -1128,6 +1173,10 @@ struct BandLaunch {
   int dh_ks, dh_kc;
   long dh_part_stride;
   AccParams e_dh_part, e_dh2_part;
+  // the previous band's K-split dH partials folded into the accumulator by
+  // nb_red workgroups (the partials alternate between two buffers)
+  DhReduce red;
+  int nb_red;
 };
 
 // One split workgroup of a K-split dH population (see BandLaunch).
@@ -1186,6 +1235,11 @@ __global__ __launch_bounds__(kWarp8 * 64) void band_kernel(BandLaunch p) {
     return;
   }
   b -= p.nb_gr;
+  if (b < p.nb_red) {
+    dh_reduce_body(p.red, b * (long)(kWarp8 * 64) + threadIdx.x, (long)p.nb_red * (kWarp8 * 64));
+    return;
+  }
+  b -= p.nb_red;
   transpose_tile<kWarp8 * 64>(p.tr.in, p.tr.ldi, p.tr.R, p.tr.C, p.tr.out, p.tr.ldo, p.tr.Rpad, (b % p.tr.tiles_r) * 64,
                               (b / p.tr.tiles_r) * 64, reinterpret_cast<bf16_t(*)[66]>(smem), threadIdx.x);
 }
@@ -1792,36 +1846,9 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(char* __restrict__ out, 
   }
 }
 
-// dH of one band split over the band's K (few row tiles): the ks fp32
-// partials P[k] = P + k * stride ([rows][d], GEMM row order) of each live row
-// are summed in fixed order and applied with the band's accumulator mode, as
-// the GEMM epilogue applies an unsplit tile: 0 out = s, 1 acc = s,
-// 2 acc += s, 3 out = acc + s; out rows go through the row map.  d % 64 == 0.
-__global__ __launch_bounds__(256) void dh_reduce_kernel(const float* __restrict__ P, long stride, int ks, int N,
-                                                        int d, const int* __restrict__ live, float* __restrict__ acc,
-                                                        int mode, void* __restrict__ out, int out_f32,
-                                                        const int* __restrict__ rowmap) {
-  const int rows = live ? min(live[0], N) : N;
-  const int q = d >> 2;
-  const long total = (long)rows * q;
-  for (long i = blockIdx.x * 256L + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
-    const int m = (int)(i / q);
-    const long o = (long)m * d + (i % q) * 4;
-    f32x4 s = *reinterpret_cast<const f32x4*>(P + o);
-    for (int k = 1; k < ks; ++k) s += *reinterpret_cast<const f32x4*>(P + k * stride + o);
-    if (mode == 1 || mode == 2) {
-      if (mode == 2) s = *reinterpret_cast<const f32x4*>(acc + o) + s;
-      *reinterpret_cast<f32x4*>(acc + o) = s;
-      continue;
-    }
-    if (mode == 3) s = *reinterpret_cast<const f32x4*>(acc + o) + s;
-    const long oo = (long)(rowmap ? rowmap[m] : m) * d + (i % q) * 4;
-    if (out_f32)
-      *reinterpret_cast<f32x4*>(static_cast<float*>(out) + oo) = s;
-    else
-      *reinterpret_cast<u32x2*>(static_cast<bf16_t*>(out) + oo) = u32x2{pack_bf16x2(s[0], s[1]),
-                                                                         pack_bf16x2(s[2], s[3])};
-  }
+// The reduction of a K-split dH as a launch of its own (after the last band).
+__global__ __launch_bounds__(256) void dh_reduce_kernel(DhReduce r) {
+  dh_reduce_body(r, blockIdx.x * 256L + threadIdx.x, (long)gridDim.x * 256);
 }
 
 // Per-row backward coefficients, for GEMM row i of source row idx[i] (idx
@@ -2086,7 +2113,8 @@ struct BwdLayout {
   int* idx;
   int* live;
   bf16_t* Hc;
-  // fp32 partials of a K-split dH (dh_ks slices of [N][d]); null when unsplit
+  // fp32 partials of a K-split dH: dh_ks slices of [N][d] per band, in two
+  // alternating buffers when there are several bands; null when unsplit
   float* dhpart;
   int dh_ks;
   size_t bytes;
@@ -2133,7 +2161,7 @@ BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bo
   L.live = compact ? c.take<int>(1) : nullptr;
   L.Hc = compact ? c.take<bf16_t>((size_t)N * d) : nullptr;
   L.dh_ks = need_dh ? dh_splits(N, d, Vb) : 1;
-  L.dhpart = L.dh_ks > 1 ? c.take<float>((size_t)L.dh_ks * N * d) : nullptr;
+  L.dhpart = L.dh_ks > 1 ? c.take<float>((size_t)(nbands > 1 ? 2 : 1) * L.dh_ks * N * d) : nullptr;
   L.bytes = align_up(c.off, 256);
   return L;
 }
@@ -2269,7 +2297,7 @@ void grad_shape(const bf16_t* H, const bf16_t* W, const float* bias, const BwdLa
 }
 
 int launch_band(const BandLaunch& p, bool has_bias, hipStream_t st) {
-  const int nb = p.nb_dw + p.nb_dw2 + p.nb_dh + p.nb_dh2 + p.nb_gr + p.nb_tr;
+  const int nb = p.nb_dw + p.nb_dw2 + p.nb_dh + p.nb_dh2 + p.nb_gr + p.nb_red + p.nb_tr;
   if (nb <= 0) return CCE_OK;
   hipEvent_t t0 = nullptr, t1 = nullptr;
   const bool timed = timing_begin(st, &t0, &t1);
@@ -2616,6 +2644,26 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
         if (rc) return rc;
       }
     }
+    // the reduction of band b's K-split dH partials, with that band's
+    // accumulator mode (as dh_shape sets it)
+    auto dh_reduction = [&](long b, int ks) {
+      DhReduce r;
+      r.P = L.dhpart + (b & 1) * (long)L.dh_ks * N * d;
+      r.stride = N * d;
+      r.ks = ks; r.N = (int)N; r.d = (int)d;
+      r.live = L.live;
+      r.acc = L.dHacc;
+      r.mode = (nbands == 1) ? 0 : (b == 0 ? 1 : (b == nbands - 1 ? 3 : 2));
+      r.out = grad_hidden;
+      r.out_f32 = (grad_hidden_dtype == CCE_DTYPE_F32);
+      r.rowmap = L.idx;
+      return r;
+    };
+    int prev_ks = 1;
+    // With many splits (very few rows) the band launches are short and the
+    // reduction rides in the next band's launch; with 2-3 splits the launches
+    // are full and it runs as a launch of its own after each band.
+    const bool fold = L.dhpart && L.dh_ks >= 4;
     for (long b = 0; b < nbands; ++b) {
       const bf16_t* G = L.G[b & 1];
       BandLaunch p = {};
@@ -2641,19 +2689,26 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
         }
         p.dh_ks = ks;
         p.dh_part_stride = N * d;
+        float* const part = L.dhpart ? L.dhpart + (b & 1) * (long)L.dh_ks * N * d : nullptr;
         if (dmain > 0) {
           dh_shape(b, G, 0, dmain, p.dh, p.e_dh);
           p.nb_dh = gm * (int)ceil_div(dmain, kFastBN) * ks;
           p.e_dh_part = p.e_dh;
-          p.e_dh_part.acc32 = L.dhpart; p.e_dh_part.ldacc = d; p.e_dh_part.mode = 1; p.e_dh_part.rowmap = nullptr;
+          p.e_dh_part.acc32 = part; p.e_dh_part.ldacc = d; p.e_dh_part.mode = 1; p.e_dh_part.rowmap = nullptr;
         }
         if (dmain < d) {
           dh_shape(b, G, dmain, d - dmain, p.dh2, p.e_dh2);
           p.nb_dh2 = gm * (int)ceil_div(d - dmain, kSlowBN) * ks;
           p.e_dh2_part = p.e_dh2;
-          p.e_dh2_part.acc32 = L.dhpart ? L.dhpart + dmain : nullptr; p.e_dh2_part.ldacc = d;
+          p.e_dh2_part.acc32 = part ? part + dmain : nullptr; p.e_dh2_part.ldacc = d;
           p.e_dh2_part.mode = 1; p.e_dh2_part.rowmap = nullptr;
         }
+        // the previous band's partials (the other buffer) into the accumulator
+        if (fold && b > 0) {
+          p.red = dh_reduction(b - 1, prev_ks);
+          p.nb_red = (int)std::min<long>(ceil_div(N * (d / 4), kWarp8 * 64 * 4), 1024);
+        }
+        prev_ks = ks;
       }
       if (b + 1 < nbands) {
         long v0, vb, vb64;
@@ -2662,12 +2717,10 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       }
       rc = launch_band(p, bias != nullptr, st);
       if (rc) return rc;
-      if (need_dh && p.dh_ks > 1) {
-        const AccParams& e = dmain > 0 ? p.e_dh : p.e_dh2;
-        const long total = N * (d / 4);
-        hipLaunchKernelGGL(dh_reduce_kernel, dim3((unsigned)std::min<long>(ceil_div(total, 256), 2048)), dim3(256), 0,
-                           st, L.dhpart, p.dh_part_stride, p.dh_ks, (int)N, (int)d, L.live, L.dHacc, e.mode,
-                           grad_hidden, (int)(grad_hidden_dtype == CCE_DTYPE_F32), L.idx);
+      if (need_dh && L.dhpart && (!fold || b + 1 == nbands)) {
+        // this band's partials (the last band's go to the output: mode 0 or 3)
+        hipLaunchKernelGGL(dh_reduce_kernel, dim3((unsigned)std::min<long>(ceil_div(N * (d / 4), 256), 2048)),
+                           dim3(256), 0, st, dh_reduction(b, prev_ks));
         HIP_TRY(hipGetLastError());
       }
       if (need_db) {
