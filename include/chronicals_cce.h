@@ -125,7 +125,10 @@ int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_
  * frozen lm_head skips grad_weight, as triton_kernels.py:3213 does).
  * grad_*_dtype selects CCE_DTYPE_BF16 or CCE_DTYPE_F32 output; grad_bias is
  * fp32.  The vocabulary is processed in bands of chunk_size columns (rounded
- * up to a multiple of 256), the reference's chunk_size argument (:1028).
+ * up to a multiple of 256; the partial band, if any, first), the reference's
+ * chunk_size argument (:1028).  Deterministic: every reduction runs in a fixed
+ * order, including the fp32 partials of dH when few rows make the library
+ * split each band's columns over several workgroups.
  */
 int cce_backward(const float* grad_out, const void* hidden, const void* weight, const void* labels,
                  int labels_int64, const float* bias, const float* lse, const int32_t* n_valid,
