@@ -1165,12 +1165,12 @@ struct BandLaunch {
   GradParams e_gr;
   TransposeParams tr;
   int nb_dw, nb_dw2, nb_dh, nb_dh2, nb_gr, nb_tr;
-  // dH split over the band's K (few row tiles): with dh_ks > 1 each dH tile
-  // has dh_ks workgroups; split k covers K columns [k*dh_kc, (k+1)*dh_kc) and
-  // writes its fp32 partial with e_dh*_part (mode 1) into slice k of the
-  // partial buffer (dh_part_stride floats apart), which dh_reduce_kernel
-  // folds into the accumulator after the launch.
-  int dh_ks, dh_kc;
+  // dH split over the band's K (few row tiles): with dh_split each dH tile
+  // has dh_ks workgroups (possibly one, for a narrow band); split k covers K
+  // columns [k*dh_kc, (k+1)*dh_kc) and writes its fp32 partial with
+  // e_dh*_part (mode 1) into slice k of the partial buffer (dh_part_stride
+  // floats apart), which a reduction folds into the accumulator afterwards.
+  int dh_split, dh_ks, dh_kc;
   long dh_part_stride;
   AccParams e_dh_part, e_dh2_part;
   // the previous band's K-split dH partials folded into the accumulator by
@@ -1212,7 +1212,7 @@ __global__ __launch_bounds__(kWarp8 * 64) void band_kernel(BandLaunch p) {
   }
   b -= p.nb_dw2;
   if (b < p.nb_dh) {
-    if (p.dh_ks > 1)
+    if (p.dh_split)
       dh_split_body<kFastBN, 2>(p.dh, p.e_dh_part, p.dh_ks, p.dh_kc, p.dh_part_stride, b, p.nb_dh, smem);
     else
       gemm_body<kFastBN, kWarp8, true, true, EpiAcc, 4>(p.dh, p.e_dh, b, p.nb_dh, smem);
@@ -1220,7 +1220,7 @@ __global__ __launch_bounds__(kWarp8 * 64) void band_kernel(BandLaunch p) {
   }
   b -= p.nb_dh;
   if (b < p.nb_dh2) {
-    if (p.dh_ks > 1)
+    if (p.dh_split)
       dh_split_body<kSlowBN, 3>(p.dh2, p.e_dh2_part, p.dh_ks, p.dh_kc, p.dh_part_stride, b, p.nb_dh2, smem);
     else
       gemm_body<kSlowBN, kWarp8, true, true, EpiAcc, 4, 3>(p.dh2, p.e_dh2, b, p.nb_dh2, smem);
@@ -2043,9 +2043,14 @@ int forward_splits(long N, long d, long V, bool compact) {
 // [256, V rounded up] and at most 2^20 columns (a band's 256-row operand
 // tiles then stay inside one buffer descriptor's 2 GB range).
 constexpr long kMaxBand = 1L << 20;
-long band_width(long V, long chunk) {
+long band_width(long V, long chunk, long N) {
   long vb = chunk <= 0 ? 8192 : (chunk > kMaxBand ? kMaxBand : chunk);
   vb = align_up((size_t)vb, 256);
+  // with few rows a band launch is short and its fixed costs dominate: up to
+  // 4x wider bands (G stays within what 4096 rows at chunk_size would take)
+  const long rows = (long)align_up((size_t)(N > 0 ? N : 1), 256);
+  const long f = std::min<long>(4, std::max<long>(1, 4096 / rows));
+  vb = std::min<long>(vb * f, std::max<long>(vb, kMaxBand / 256 * 256));
   const long vmax = (long)align_up((size_t)V, 256);
   if (vb > vmax) vb = vmax;
   if (vb < 256) vb = 256;
@@ -2385,7 +2390,7 @@ int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_
   if (!bytes) return fail(CCE_ERR_INVALID_ARG, "bytes must not be null");
   int rc = check_dims(N, d, V);
   if (rc) return rc;
-  *bytes = bwd_layout(nullptr, N, d, V, band_width(V, chunk_size), need_grad_hidden != 0, need_grad_weight != 0).bytes;
+  *bytes = bwd_layout(nullptr, N, d, V, band_width(V, chunk_size, N), need_grad_hidden != 0, need_grad_weight != 0).bytes;
   return CCE_OK;
 }
 
@@ -2508,7 +2513,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
   const bool need_dh = grad_hidden != nullptr, need_dw = grad_weight != nullptr, need_db = grad_bias != nullptr;
   if (need_db && !bias) return fail(CCE_ERR_INVALID_ARG, "grad_bias requested without bias");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const long Vb = band_width(V, chunk_size);
+  const long Vb = band_width(V, chunk_size, N);
   const BwdLayout need = bwd_layout(nullptr, N, d, V, Vb, need_dh, need_dw);
   if (workspace_bytes < need.bytes || (need.bytes && !workspace))
     return fail(CCE_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need.bytes, workspace_bytes);
@@ -2687,6 +2692,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
           p.dh_kc = (int)align_up((size_t)ceil_div(vb64, L.dh_ks), 64);
           ks = (int)ceil_div(vb64, p.dh_kc);
         }
+        p.dh_split = L.dhpart != nullptr;  // every band, even one left with a single split
         p.dh_ks = ks;
         p.dh_part_stride = N * d;
         float* const part = L.dhpart ? L.dhpart + (b & 1) * (long)L.dh_ks * N * d : nullptr;

@@ -100,6 +100,8 @@ def test_ragged_shapes(gpu, N, d, V, chunk):
     (600, 320, 9000, 4096, torch.bfloat16, "mean", 0.7),
     # one band (mode 0: straight to the output; the band is 3072 wide): 6 splits of 512 columns, the last shorter
     (130, 512, 3000, 8192, torch.bfloat16, "sum", 0.1),
+    # V = 8 * 8192 + 40 = 2 * 32768 + 40: a 40-column first band left with a single split still writes partials
+    (256, 768, 65576, 8192, torch.bfloat16, "mean", 0.1),
 ])
 def test_small_batch_split_dh(gpu, N, d, V, chunk, hdtype, reduction, ignore_frac):
     """With few 256-row tiles the banded dH splits each band's K over several
