@@ -2043,13 +2043,14 @@ int forward_splits(long N, long d, long V, bool compact) {
 // [256, V rounded up] and at most 2^20 columns (a band's 256-row operand
 // tiles then stay inside one buffer descriptor's 2 GB range).
 constexpr long kMaxBand = 1L << 20;
-long band_width(long V, long chunk, long N) {
+long band_width(long V, long chunk, long N, long d) {
   long vb = chunk <= 0 ? 8192 : (chunk > kMaxBand ? kMaxBand : chunk);
   vb = align_up((size_t)vb, 256);
   // with few rows a band launch is short and its fixed costs dominate: up to
-  // 4x wider bands (G stays within what 4096 rows at chunk_size would take)
+  // 4x wider bands, while the band buffers (G: rows x band, W^T: d x band)
+  // stay within what 4096 rows take at chunk_size
   const long rows = (long)align_up((size_t)(N > 0 ? N : 1), 256);
-  const long f = std::min<long>(4, std::max<long>(1, 4096 / rows));
+  const long f = std::min<long>(4, std::max<long>(1, (4096 + d) / (rows + d)));
   vb = std::min<long>(vb * f, std::max<long>(vb, kMaxBand / 256 * 256));
   const long vmax = (long)align_up((size_t)V, 256);
   if (vb > vmax) vb = vmax;
@@ -2390,7 +2391,7 @@ int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_
   if (!bytes) return fail(CCE_ERR_INVALID_ARG, "bytes must not be null");
   int rc = check_dims(N, d, V);
   if (rc) return rc;
-  *bytes = bwd_layout(nullptr, N, d, V, band_width(V, chunk_size, N), need_grad_hidden != 0, need_grad_weight != 0).bytes;
+  *bytes = bwd_layout(nullptr, N, d, V, band_width(V, chunk_size, N, d), need_grad_hidden != 0, need_grad_weight != 0).bytes;
   return CCE_OK;
 }
 
@@ -2513,7 +2514,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
   const bool need_dh = grad_hidden != nullptr, need_dw = grad_weight != nullptr, need_db = grad_bias != nullptr;
   if (need_db && !bias) return fail(CCE_ERR_INVALID_ARG, "grad_bias requested without bias");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const long Vb = band_width(V, chunk_size, N);
+  const long Vb = band_width(V, chunk_size, N, d);
   const BwdLayout need = bwd_layout(nullptr, N, d, V, Vb, need_dh, need_dw);
   if (workspace_bytes < need.bytes || (need.bytes && !workspace))
     return fail(CCE_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need.bytes, workspace_bytes);
