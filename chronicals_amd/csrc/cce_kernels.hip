@@ -2048,9 +2048,10 @@ long band_width(long V, long chunk, long N, long d) {
   vb = align_up((size_t)vb, 256);
   // with few rows a band launch is short and its fixed costs dominate: up to
   // 4x wider bands, while the band buffers (G: rows x band, W^T: d x band)
-  // stay within what 4096 rows take at chunk_size
+  // stay within what 4096 rows take at chunk_size.  Below 1024 rows W^T and
+  // the dH partials would outgrow the logits themselves, for no measured gain.
   const long rows = (long)align_up((size_t)(N > 0 ? N : 1), 256);
-  const long f = std::min<long>(4, std::max<long>(1, (4096 + d) / (rows + d)));
+  const long f = rows < 1024 ? 1 : std::min<long>(4, std::max<long>(1, (4096 + d) / (rows + d)));
   vb = std::min<long>(vb * f, std::max<long>(vb, kMaxBand / 256 * 256));
   const long vmax = (long)align_up((size_t)V, 256);
   if (vb > vmax) vb = vmax;

@@ -126,8 +126,9 @@ int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_
  * grad_*_dtype selects CCE_DTYPE_BF16 or CCE_DTYPE_F32 output; grad_bias is
  * fp32.  The vocabulary is processed in bands of chunk_size columns (rounded
  * up to a multiple of 256; the partial band, if any, first), the reference's
- * chunk_size argument (:1028); with few rows the bands are up to 4x wider,
- * while G and W^T of a band take no more than at 4096 rows and chunk_size.  Deterministic: every reduction runs in a fixed
+ * chunk_size argument (:1028); from 1024 to 4095 rows the bands are up to
+ * 4x wider, while G and W^T of a band take no more than at 4096 rows and
+ * chunk_size.  Deterministic: every reduction runs in a fixed
  * order, including the fp32 partials of dH when few rows make the library
  * split each band's columns over several workgroups.
  */
