@@ -92,6 +92,21 @@ def test_abi_version(lib):
     assert lib.cce_abi_version() == header_define("CCE_ABI_VERSION")
 
 
+@pytest.mark.parametrize("d,V", [(896, 151936), (4096, 128256), (768, 50257), (3584, 152064)])
+def test_small_batch_backward_workspace_bounded(lib, d, V):
+    """Small batches widen the vocabulary bands (from 1024 rows) and split dH
+    into fp32 partials (few row tiles); neither may make a smaller batch need
+    more backward workspace than 4096 rows at the same chunk_size, and below
+    1024 rows none of it may outgrow the materialised fp32 logits and their
+    gradient."""
+    ref = _lib.backward_workspace_bytes(4096, d, V, 8192, True, True)
+    for N in (1, 256, 512, 1024, 2048, 3072):
+        ws = _lib.backward_workspace_bytes(N, d, V, 8192, True, True)
+        assert 0 < ws <= ref, (N, ws, ref)
+    if d <= 1024:
+        assert _lib.backward_workspace_bytes(256, d, V, 8192, True, True) < 256 * V * 8
+
+
 def test_workspace_queries(lib):
     f1 = _lib.forward_workspace_bytes(1024, 896, 151936, _lib.CCE_REDUCTION_MEAN)
     f2 = _lib.forward_workspace_bytes(2048, 896, 151936, _lib.CCE_REDUCTION_MEAN)
