@@ -2032,7 +2032,10 @@ int lse_bn(long d) { return fast_k(d) ? kFastBN : kSlowBN; }
 int forward_splits(long N, long d, long V, bool compact) {
   if (N <= 0) return 1;
   const long gm = ceil_div(N, kBM), tn = ceil_div(V, lse_bn(d));
-  long s = ceil_div(2048, gm);
+  // about 512 workgroups for few row tiles (runs of several vocabulary tiles,
+  // so the pipeline's start is paid once per run), never fewer splits than
+  // min(32, 2048 / row tiles): large batches keep their split counts
+  long s = std::max(ceil_div(512, gm), std::min<long>(32, ceil_div(2048, gm)));
   if (compact && s < 32) s = 32;
   if (s > tn) s = tn;
   if (s < 1) s = 1;
