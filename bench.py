@@ -36,6 +36,12 @@ if REPO not in sys.path:
     sys.path.insert(0, REPO)
 
 PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 4096 FLOP/clk x 2.4 GHz (dense bf16 MFMA)
+# The rate a 256 x 256-tile bf16 MFMA loop reaches on this chip with random
+# operands (LDS pre-filled, no global memory; the chip is power-limited and
+# clocks down with the operands' bit activity): measured 1616-1660 TFLOP/s.
+# A design that recomputes the logits executes 8*N*V*d for 6*N*V*d credited,
+# so its step cannot exceed 6/8 of this.
+CEILING_BF16_TFLOPS = 1640.0
 PEAK_HBM_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 TRAFFIC_LOGITS_FILE = os.path.join(REPO, "profiles", "traffic_logits.json")
@@ -80,14 +86,35 @@ def kernel_timed_steps(step, steps: int) -> None:
 
 
 def cpu_model() -> str:
+    """CPU model string with the host's logical CPU count and the CPUs this process may run on."""
+    name = None
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                    name = line.split(":", 1)[1].strip()
+                    break
     except OSError:
         pass
-    return platform.processor() or "unknown"
+    name = name or platform.processor() or "unknown"
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = None
+    return f"{name} ({os.cpu_count()} logical CPUs on the host, {allowed} usable by this process)"
+
+
+def blas_threads() -> int:
+    """Threads the BLAS under numpy uses (threadpoolctl), else OMP_NUM_THREADS / the CPU count."""
+    try:
+        from threadpoolctl import threadpool_info
+        blas = [p for p in threadpool_info() if p.get("user_api") == "blas"]
+        mine = [p for p in blas if "numpy" in p.get("filepath", "")] or blas
+        if mine:
+            return int(mine[0]["num_threads"])
+    except Exception:  # noqa: BLE001 - threadpoolctl is optional
+        pass
+    return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
 
 
 def cpu_baseline(cfg, rows: int, seed: int = 0) -> dict:
@@ -99,7 +126,7 @@ def cpu_baseline(cfg, rows: int, seed: int = 0) -> dict:
     hn = h.float().numpy()
     wn = w.float().numpy()
     ln = lab.numpy()
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    threads = blas_threads()
     warm = max(8, rows // 8)
     cce_oracle.loss_and_grads(hn[:warm], wn, ln[:warm], chunk_size=8192)
     times = []
@@ -206,6 +233,11 @@ def main() -> int:
                     help="only run a plain device copy of BYTES (PMC calibration) and exit")
     ap.add_argument("--frozen-weight", action="store_true",
                     help="lm_head weight frozen (LoRA): the step computes dHidden only, 4*N*V*d credited FLOPs")
+    ap.add_argument("--trainer", action="store_true",
+                    help="the reference trainer's call (chronicals_trainer.py:577-594, :1747-1771): fp32 hidden "
+                         "states and fp32 master lm_head weight under bf16 autocast (cast to bf16 per call, fp32 "
+                         "gradients), chunk from get_optimal_chunk_size, z_loss_weight 1e-4, through "
+                         "CutCrossEntropyLoss")
     ap.add_argument("--blas-reference", action="store_true",
                     help="only time torch.matmul (hipBLASLt) on the path's GEMM shapes and exit")
     ap.add_argument("--workload", choices=("fused", "logits", "logits-fused"), default="fused",
@@ -232,15 +264,21 @@ def main() -> int:
     import torch
 
     from chronicals_amd import _lib
-    from chronicals_amd.kernels.cut_cross_entropy import cut_cross_entropy
+    from chronicals_amd.kernels.cut_cross_entropy import (CutCrossEntropyLoss, cut_cross_entropy,
+                                                          get_optimal_chunk_size)
     from tests.cce_common import CONFIGS, make_inputs
 
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     h, w, lab = make_inputs(cfg, seed=0, device=dev, gen_device="cuda")
-    h = h.to(torch.bfloat16).requires_grad_(True)
-    w = w.to(torch.bfloat16).requires_grad_(not args.frozen_weight)
+    # the configuration's input dtype goes through the boundary as it is: C1's
+    # fp32 operands are rounded to bf16 inside the op (bf16 MFMA arithmetic with
+    # fp32 accumulation) and get fp32 gradients back; the trainer mode keeps
+    # fp32 hidden states and an fp32 master weight
+    io_dtype = torch.float32 if args.trainer else cfg.dtype
+    h = h.to(io_dtype).requires_grad_(True)
+    w = w.to(io_dtype).requires_grad_(not args.frozen_weight)
     N, d, V = cfg.N, cfg.d, cfg.V
     credited_step = (4.0 if args.frozen_weight else 6.0) * N * V * d
     # forward and backward skip the row tiles past the labelled rows (the
@@ -248,11 +286,21 @@ def main() -> int:
     # rows only is reported beside
     n_valid = int((lab != -100).sum())
     credited_valid = (4.0 if args.frozen_weight else 6.0) * n_valid * V * d
+    chunk = get_optimal_chunk_size(V, d) if args.trainer else args.chunk
+    z_loss = 1e-4 if args.trainer else 0.0
+    loss_fn = CutCrossEntropyLoss(chunk_size=None, ignore_index=-100, z_loss_weight=z_loss,
+                                  reduction=cfg.reduction) if args.trainer else None
 
     def step():
         h.grad = None
         w.grad = None
-        loss = cut_cross_entropy(h, w, lab, None, args.chunk, -100, 0.0, 0.0, reduction=cfg.reduction)
+        if args.trainer:
+            # chronicals_trainer.py:1747-1771: the loss runs under bf16 autocast on
+            # the model's fp32 hidden states and lm_head.weight
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                loss = loss_fn(h, w, lab, None)
+        else:
+            loss = cut_cross_entropy(h, w, lab, None, chunk, -100, 0.0, z_loss, reduction=cfg.reduction)
         loss.backward()
         return loss
 
@@ -295,13 +343,32 @@ def main() -> int:
     try:
         with open(TRAFFIC_FILE) as f:
             tr = json.load(f)
-        if tr.get("config") == cfg.name and tr.get("kernel") == dom and not args.frozen_weight:
+        if (tr.get("config") == cfg.name and tr.get("kernel") == dom and not args.frozen_weight
+                and not args.trainer and chunk == tr.get("chunk_size", 8192)):
             traffic = tr.get("hbm_bytes_per_launch")
             clock = tr.get("mfma_busy_and_clock", {}).get(dom, {}).get("clock_ghz")
     except (OSError, ValueError):
         pass
 
     step_tflops = credited_step / (ms * 1e-3) / 1e12
+    # the same kernel over the labelled rows only (the GEMMs skip the 256-row
+    # tiles past them; the last live tile is counted whole)
+    valid_frac = min(1.0, (-(-n_valid // 256) * 256) / N)
+    # ceiling of this kernel kind: the random-operand MFMA loop rate scaled by
+    # its credited share of the executed FLOPs
+    ceiling = CEILING_BF16_TFLOPS * kd["tflops_credited"] / kd["tflops_executed"]
+    step_ceiling = CEILING_BF16_TFLOPS * (4.0 if args.frozen_weight else 6.0) / (6.0 if args.frozen_weight else 8.0)
+    if args.trainer:
+        workload = (f"{cfg.name} in the reference trainer's call: CutCrossEntropyLoss(chunk_size=None -> {chunk}, "
+                    f"z_loss_weight=1e-4) on fp32 hidden [{N}, {d}] and an fp32 master lm_head weight [{V}, {d}] "
+                    f"under bf16 autocast (both cast to bf16 per call, bf16 MFMA with fp32 accumulation, fp32 "
+                    f"dHidden and dW), {int(cfg.ignore_frac * 100)}% ignore_index, {cfg.reduction}")
+    else:
+        workload = (f"{cfg.name}: fused linear-CE fwd+bwd N={N} d={d} V={V} "
+                    + ("fp32 inputs (rounded to bf16 at the boundary: bf16 MFMA with fp32 accumulation; fp32 "
+                       "gradients)" if io_dtype == torch.float32 else "bf16")
+                    + f", {int(cfg.ignore_frac * 100)}% ignore_index, {cfg.reduction}; grads "
+                    + ("dHidden only (frozen lm_head weight)" if args.frozen_weight else "dHidden, dW"))
     out = {
         "metric": "fused linear-CE fwd+bwd tokens/s and % bf16 MFMA peak, N=16k V=152k",
         "value": N / (ms * 1e-3),
@@ -316,16 +383,22 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) hidden, N(0,0.02) W, uniform labels, 5% ignore_index)",
-        "config": {"workload": f"{cfg.name}: fused linear-CE fwd+bwd N={N} d={d} V={V} bf16, "
-                               f"{int(cfg.ignore_frac * 100)}% ignore_index, {cfg.reduction}; grads "
-                               + ("dHidden only (frozen lm_head weight)" if args.frozen_weight else "dHidden, dW"),
-                   "N": N, "d": d, "V": V, "chunk_size": args.chunk, "frozen_weight": bool(args.frozen_weight)},
+        "config": {"workload": workload, "N": N, "d": d, "V": V, "chunk_size": chunk,
+                   "frozen_weight": bool(args.frozen_weight), "trainer_call": bool(args.trainer),
+                   "input_dtype": str(io_dtype).replace("torch.", ""), "z_loss_weight": z_loss},
         "pct_bf16_peak": 100.0 * step_tflops / PEAK_BF16_TFLOPS,
         "step_tflops_algorithmic": step_tflops,
         "valid_rows": n_valid,
         "pct_bf16_peak_valid_rows": 100.0 * credited_valid / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+        # the step against the random-operand MFMA ceiling times the credited
+        # share of a recomputing design's executed work (6/8; frozen W 4/6)
+        "step_ceiling_tflops": step_ceiling,
+        "pct_of_step_ceiling": 100.0 * step_tflops / step_ceiling,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
+                     "ceiling": ceiling, "frac_of_ceiling": achieved / ceiling,
+                     "achieved_valid_rows": achieved * valid_frac,
+                     "frac_valid_rows": achieved * valid_frac / PEAK_BF16_TFLOPS,
                      # the chip runs below its 2.4 GHz peak clock under this load (power-limited); the
                      # clock the profile measured for this kernel, and the fraction of the peak at it
                      "clock_ghz_profiled": clock,

@@ -2144,6 +2144,11 @@ long band_dmain(long d) { return (d % 256 == 0 || d % 256 > 128) ? d : d - d % 2
 // K is split so that tiles x splits reaches about 128 workgroups, with at
 // least 8 slabs of 64 per split (more splits cost more in the fp32 partials'
 // reduction than their shorter K loops return).
+// With 4 or more K splits (very few rows) the band launches are short, and
+// each band's dH reduction rides in the next band's launch (two partial
+// buffers, alternating); with 2-3 splits it is a launch of its own.
+bool dh_fold(int ks) { return ks >= 4; }
+
 int dh_splits(long N, long d, long Vb) {
   if (!banded(d) || N <= 0 || d <= 0) return 1;
   const long dmain = band_dmain(d);
@@ -2171,7 +2176,11 @@ BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bo
   L.live = compact ? c.take<int>(1) : nullptr;
   L.Hc = compact ? c.take<bf16_t>((size_t)N * d) : nullptr;
   L.dh_ks = need_dh ? dh_splits(N, d, Vb) : 1;
-  L.dhpart = L.dh_ks > 1 ? c.take<float>((size_t)(nbands > 1 ? 2 : 1) * L.dh_ks * N * d) : nullptr;
+  // a second partial buffer only when the reduction rides in the next band's
+  // launch (dh_fold); otherwise each band's reduction runs before the next
+  // band launch writes the one buffer again
+  L.dhpart = L.dh_ks > 1 ? c.take<float>((size_t)(dh_fold(L.dh_ks) && nbands > 1 ? 2 : 1) * L.dh_ks * N * d)
+                         : nullptr;
   L.bytes = align_up(c.off, 256);
   return L;
 }
@@ -2656,9 +2665,15 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     }
     // the reduction of band b's K-split dH partials, with that band's
     // accumulator mode (as dh_shape sets it)
+    // With 4 or more splits (very few rows) the band launches are short and the
+    // reduction rides in the next band's launch, so the partials alternate
+    // between two buffers; with 2-3 splits the launches are full and it runs
+    // as a launch of its own after each band, on the one buffer.
+    const bool fold = L.dhpart && dh_fold(L.dh_ks);
+    auto dh_part = [&](long b) { return L.dhpart + (fold ? (b & 1) : 0) * (long)L.dh_ks * N * d; };
     auto dh_reduction = [&](long b, int ks) {
       DhReduce r;
-      r.P = L.dhpart + (b & 1) * (long)L.dh_ks * N * d;
+      r.P = dh_part(b);
       r.stride = N * d;
       r.ks = ks; r.N = (int)N; r.d = (int)d;
       r.live = L.live;
@@ -2670,10 +2685,6 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       return r;
     };
     int prev_ks = 1;
-    // With many splits (very few rows) the band launches are short and the
-    // reduction rides in the next band's launch; with 2-3 splits the launches
-    // are full and it runs as a launch of its own after each band.
-    const bool fold = L.dhpart && L.dh_ks >= 4;
     for (long b = 0; b < nbands; ++b) {
       const bf16_t* G = L.G[b & 1];
       BandLaunch p = {};
@@ -2700,7 +2711,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
         p.dh_split = L.dhpart != nullptr;  // every band, even one left with a single split
         p.dh_ks = ks;
         p.dh_part_stride = N * d;
-        float* const part = L.dhpart ? L.dhpart + (b & 1) * (long)L.dh_ks * N * d : nullptr;
+        float* const part = L.dhpart ? dh_part(b) : nullptr;
         if (dmain > 0) {
           dh_shape(b, G, 0, dmain, p.dh, p.e_dh);
           p.nb_dh = gm * (int)ceil_div(dmain, kFastBN) * ks;

@@ -42,6 +42,9 @@ TRITON_BLOCK_SIZE_MAX = 65536 // 2
 
 __all__ = [
     "cut_cross_entropy",
+    "linear_cross_entropy",
+    "cce_forward_pytorch",
+    "cce_backward_pytorch",
     "chunked_cross_entropy_loss",
     "ChunkedCrossEntropyLoss",
     "CutCrossEntropyLoss",
@@ -302,6 +305,37 @@ def cut_cross_entropy(
                                          z_loss_weight, reduction)
 
 
+def linear_cross_entropy(
+    hidden: torch.Tensor,
+    weight: torch.Tensor,
+    labels: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+    ignore_index: int = -100,
+    reduction: str = "mean",
+    *,
+    chunk_size: int = DEFAULT_VOCAB_CHUNK_SIZE,
+    label_smoothing: float = 0.0,
+    z_loss_weight: float = 0.0,
+) -> torch.Tensor:
+    """``cut_cross_entropy`` in the (hidden, weight, labels, bias, ignore_index,
+    reduction) argument order.
+
+    The reference imports this name from its cut_cross_entropy module
+    (chronicals_trainer.py:79-89, triton_kernels.py:44-58) but never defines
+    it, so those imports fail there and the trainer falls back to its
+    non-fused losses.  Here the name exists, so the same import block
+    resolves against this package.
+    """
+    return CutCrossEntropyFunction.apply(hidden, weight, labels, bias, chunk_size, ignore_index, label_smoothing,
+                                         z_loss_weight, reduction)
+
+
+# The static forward / backward passes under the names triton_kernels.py:50-51
+# imports from the reference module (which does not define them either).
+cce_forward_pytorch = CutCrossEntropyForward.forward
+cce_backward_pytorch = CutCrossEntropyBackward.backward
+
+
 class CutCrossEntropyLoss(nn.Module):
     """nn.Module wrapper (reference cut_cross_entropy.py:1081-1162).
 
@@ -383,8 +417,11 @@ def compute_z_loss(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Ten
                    chunk_size: int = 8192) -> torch.Tensor:
     """Mean over valid rows of lse^2 (reference cut_cross_entropy.py:1379-1400).
 
-    Not differentiable (the reference's is not either: it runs the forward
-    pass only).  ``chunk_size`` is accepted for signature compatibility.
+    A monitoring value: it is returned without autograd history.  The
+    reference computes it with its plain-torch forward, which autograd would
+    track on its CPU path; the fused kernels here have no gradient for the
+    z-loss term alone.  ``chunk_size`` is accepted for signature
+    compatibility.
     """
     del chunk_size
     _, lse, _, _, _, lab, _, _ = _forward_raw(hidden, weight, labels, bias, ignore_index, 0.0, 0.0,

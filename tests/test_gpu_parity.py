@@ -100,8 +100,14 @@ def test_ragged_shapes(gpu, N, d, V, chunk):
     (600, 320, 9000, 4096, torch.bfloat16, "mean", 0.7),
     # one band (mode 0: straight to the output; the band is 3072 wide): 6 splits of 512 columns, the last shorter
     (130, 512, 3000, 8192, torch.bfloat16, "sum", 0.1),
-    # V = 8 * 8192 + 40 = 2 * 32768 + 40: a 40-column first band left with a single split still writes partials
+    # V = 8 * 8192 + 40: 9 bands of 8192 (256 rows are not widened); the 40-column first band is left with a
+    # single split and still writes partials
     (256, 768, 65576, 8192, torch.bfloat16, "mean", 0.1),
+    # 1100 rows widen chunk 1024 to 3072-column bands: 7 bands; d = 128 is one 128-wide tail tile (5 dH tiles,
+    # 6 K splits: the reduction rides in the next band's launch); 30% of the rows ignored
+    (1100, 128, 20000, 1024, torch.bfloat16, "mean", 0.3),
+    # 1300 rows widen chunk 2048 to 4096: 3 bands (a 808-column first band); 6 dH tiles of 256 columns, 8 splits
+    (1300, 256, 9000, 2048, torch.float32, "sum", 0.1),
 ])
 def test_small_batch_split_dh(gpu, N, d, V, chunk, hdtype, reduction, ignore_frac):
     """With few 256-row tiles the banded dH splits each band's K over several
@@ -156,9 +162,11 @@ def test_all_ignored(gpu):
 def test_ignored_row_tiles_are_skipped(gpu, reduction, bias, hdtype):
     # The banded backward compacts the labelled rows to the front and skips
     # the 256-row tiles past them: 400 labelled rows of 1100 leave 2 of 5 row
-    # tiles live.  The ignored rows' dH must still be exactly zero.
+    # tiles live.  The ignored rows' dH must still be exactly zero.  V = 9500
+    # keeps 4 bands (1100 rows widen chunk 1024 to 3072-column bands), so the
+    # accumulator modes 1, 2 and 3 all run on the compacted rows.
     print(f"case compaction reduction={reduction} bias={bias} hdtype={hdtype}", flush=True)
-    h, w, lab, b = _rand_case(1100, 128, 3000, seed=21, ignore_frac=0.0, bias=bias)
+    h, w, lab, b = _rand_case(1100, 128, 9500, seed=21, ignore_frac=0.0, bias=bias)
     g = torch.Generator().manual_seed(4)
     lab[torch.randperm(1100, generator=g)[:700]] = IGNORE
     go = torch.rand(1100, generator=g) if reduction == "none" else 1.3
@@ -188,10 +196,11 @@ def test_labelled_rows_at_the_end(gpu):
 def test_forward_lse_labelled_rows(gpu, d):
     """CCE_LSE_LABELLED_ROWS: the same loss and n_valid as CCE_LSE_ALL_ROWS, the
     same lse / target on labelled rows, 0 on ignored rows (d = 128 compacts
-    the rows; d = 72 runs the register-staged GEMM over every row)."""
+    the rows; d = 72 runs the register-staged GEMM over every row).  V = 9500
+    gives the autograd check 4 backward bands of 3072 columns."""
     from chronicals_amd import _lib
     print(f"case lse_rows d={d}", flush=True)
-    h, w, lab, b = _rand_case(1100, d, 3000, seed=29, ignore_frac=0.0, bias=True)
+    h, w, lab, b = _rand_case(1100, d, 9500, seed=29, ignore_frac=0.0, bias=True)
     g = torch.Generator().manual_seed(8)
     lab[torch.randperm(1100, generator=g)[:650]] = IGNORE
     hd, wd, ld, bd = h.to(gpu, torch.bfloat16), w.to(gpu, torch.bfloat16), lab.to(gpu), b.to(gpu)
@@ -494,3 +503,39 @@ def test_fused_extreme_logit_magnitudes(gpu, scale):
     assert_loss_close(got["loss"], ref["loss"], "loss")
     assert_grad_close(got["dh"], ref["dh"], "dh")
     assert_grad_close(got["dw"], ref["dw"], "dw")
+
+
+@pytest.mark.parametrize("ignore_frac,bias", [(0.0, False), (0.4, True), (1.0, False)])
+def test_compute_z_loss(gpu, ignore_frac, bias):
+    """compute_z_loss (reference cut_cross_entropy.py:1379-1400) = mean over the
+    labelled rows of lse^2, against the oracle's lse; every row ignored gives 0
+    (the reference's denominator is clamped to 1)."""
+    from chronicals_amd.kernels.cut_cross_entropy import compute_z_loss
+    print(f"case compute_z_loss ignore_frac={ignore_frac} bias={bias}", flush=True)
+    h, w, lab, b = _rand_case(700, 192, 5001, seed=41, ignore_frac=ignore_frac, bias=bias)
+    got = compute_z_loss(h.to(gpu, torch.bfloat16), w.to(gpu, torch.bfloat16), lab.to(gpu),
+                         None if b is None else b.to(gpu))
+    ref = run_oracle(h, w, lab, b)
+    valid = (lab != IGNORE).numpy()
+    want = float((ref["lse"][valid] ** 2).sum() / max(valid.sum(), 1))
+    assert not got.requires_grad
+    if valid.any():
+        assert_loss_close(float(got), want, "z-loss")
+    else:
+        assert float(got) == 0.0
+
+
+def test_linear_cross_entropy_name(gpu):
+    """linear_cross_entropy (the name the reference's trainer imports) takes
+    (hidden, weight, labels, bias, ignore_index, reduction) and gives
+    cut_cross_entropy's loss and gradients."""
+    from chronicals_amd.kernels.cut_cross_entropy import linear_cross_entropy
+    h, w, lab, b = _rand_case(300, 128, 3001, seed=43, bias=True)
+    hd = h.to(gpu, torch.bfloat16).requires_grad_(True)
+    wd = w.to(gpu, torch.bfloat16).requires_grad_(True)
+    bd = b.to(gpu).requires_grad_(True)
+    loss = linear_cross_entropy(hd, wd, lab.to(gpu), bd, IGNORE, "sum")
+    loss.backward()
+    got = {"loss": loss.detach().cpu().numpy(), "dh": hd.grad.float().cpu().numpy(),
+           "dw": wd.grad.float().cpu().numpy(), "db": bd.grad.float().cpu().numpy()}
+    compare(got, run_oracle(h, w, lab, b, reduction="sum"), "linear_cross_entropy")

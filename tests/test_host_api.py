@@ -269,3 +269,28 @@ def test_reference_module_public_names_all_present():
             a.z_loss_weight) == (32000, 100000, -100, 0.0, 0.0)
     with pytest.raises(RuntimeError, match="HIP devices"):
         a(torch.randn(4, 8), torch.randn(40000, 8), torch.zeros(4, dtype=torch.long))
+
+
+def test_reference_import_blocks_resolve():
+    # the names chronicals_trainer.py:79-89 and triton_kernels.py:44-58 import
+    # from the reference module; with this package's module path they resolve
+    from chronicals_amd.kernels.cut_cross_entropy import (  # noqa: F401
+        CutCrossEntropyFunction,
+        CutCrossEntropyLoss,
+        DEFAULT_VOCAB_CHUNK_SIZE,
+        cce_backward_pytorch,
+        cce_forward_pytorch,
+        cut_cross_entropy,
+        estimate_memory_savings,
+        get_optimal_chunk_size,
+        linear_cross_entropy,
+    )
+    assert cce_forward_pytorch is cce.CutCrossEntropyForward.forward
+    assert cce_backward_pytorch is cce.CutCrossEntropyBackward.backward
+    sig = list(inspect.signature(linear_cross_entropy).parameters)
+    assert sig[:6] == ["hidden", "weight", "labels", "bias", "ignore_index", "reduction"]
+    with pytest.raises(RuntimeError, match="HIP devices"):
+        linear_cross_entropy(torch.randn(4, 8), torch.randn(10, 8), torch.zeros(4, dtype=torch.long))
+    with pytest.raises(ValueError):
+        linear_cross_entropy(torch.randn(4, 8), torch.randn(10, 8), torch.zeros(4, dtype=torch.long),
+                             reduction="avg")
