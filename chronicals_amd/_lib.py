@@ -11,7 +11,7 @@ import threading
 from . import build as _build
 
 # constants mirrored from include/chronicals_cce.h
-CCE_ABI_VERSION = 4
+CCE_ABI_VERSION = 5
 CCE_OK = 0
 CCE_ERR_INVALID_ARG = 1
 CCE_ERR_WORKSPACE = 2
@@ -26,6 +26,7 @@ CCE_SMOOTH_LOGV = 0
 CCE_SMOOTH_UNIFORM = 1
 CCE_LSE_ALL_ROWS = 0
 CCE_LSE_LABELLED_ROWS = 1
+CCE_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 CCE_KERNEL_FWD_LSE = 0
 CCE_KERNEL_BWD_GRAD = 1
@@ -62,6 +63,13 @@ SIGNATURES = {
         _f32, _f32, _i32, _i32, _i32,        # label_smoothing, z_loss_weight, smoothing_form, reduction, lse_rows
         _vp, _vp, _vp, _vp,                  # loss_out, lse_out, target_out, n_valid_out
         _vp, _sz, _vp,                       # workspace, workspace_bytes, stream
+    ]),
+    "cce_forward_noalloc": (_i32, [
+        _vp, _vp, _vp, _i32, _vp,            # hidden, weight, labels, labels_int64, bias
+        _i64, _i64, _i64, _i64,              # N, d, V, ignore_index
+        _f32, _f32, _i32, _i32, _i32,        # label_smoothing, z_loss_weight, smoothing_form, reduction, lse_rows
+        _vp, _vp, _vp, _vp,                  # loss_out, lse_out, target_out, n_valid_out
+        _vp,                                 # stream
     ]),
     "cce_backward": (_i32, [
         _vp, _vp, _vp, _vp, _i32, _vp,       # grad_out, hidden, weight, labels, labels_int64, bias

@@ -2373,46 +2373,10 @@ int check_logits_args(long N, long V, int dtype, long ld, int reduction, float e
   return CCE_OK;
 }
 
-}  // namespace
-
-// ===========================================================================
-// C ABI
-// ===========================================================================
-
-extern "C" {
-
-const char* cce_last_error(void) { return g_err; }
-
-int cce_abi_version(void) { return CCE_ABI_VERSION; }
-
-int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, int lse_rows, size_t* bytes) {
-  g_err[0] = 0;
-  if (!bytes) return fail(CCE_ERR_INVALID_ARG, "bytes must not be null");
-  int rc = check_dims(N, d, V);
-  if (rc) return rc;
-  if (reduction < CCE_REDUCTION_NONE || reduction > CCE_REDUCTION_SUM)
-    return fail(CCE_ERR_INVALID_ARG, "reduction must be 0 (none), 1 (mean) or 2 (sum), got %d", reduction);
-  if (lse_rows != CCE_LSE_ALL_ROWS && lse_rows != CCE_LSE_LABELLED_ROWS)
-    return fail(CCE_ERR_INVALID_ARG, "lse_rows must be CCE_LSE_ALL_ROWS or CCE_LSE_LABELLED_ROWS, got %d", lse_rows);
-  *bytes = fwd_layout(nullptr, N, d, V, reduction, lse_rows).bytes;
-  return CCE_OK;
-}
-
-int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_size, int need_grad_hidden,
-                                 int need_grad_weight, size_t* bytes) {
-  g_err[0] = 0;
-  if (!bytes) return fail(CCE_ERR_INVALID_ARG, "bytes must not be null");
-  int rc = check_dims(N, d, V);
-  if (rc) return rc;
-  *bytes = bwd_layout(nullptr, N, d, V, band_width(V, chunk_size, N, d), need_grad_hidden != 0, need_grad_weight != 0).bytes;
-  return CCE_OK;
-}
-
-int cce_forward(const void* hidden, const void* weight, const void* labels, int labels_int64, const float* bias,
+int forward_run(const void* hidden, const void* weight, const void* labels, int labels_int64, const float* bias,
                 int64_t N, int64_t d, int64_t V, int64_t ignore_index, float label_smoothing, float z_loss_weight,
                 int smoothing_form, int reduction, int lse_rows, float* loss_out, float* lse_out, float* target_out,
                 int32_t* n_valid_out, void* workspace, size_t workspace_bytes, void* stream) {
-  g_err[0] = 0;
   int rc = check_dims(N, d, V);
   if (rc) return rc;
   if (smoothing_form != CCE_SMOOTH_LOGV && smoothing_form != CCE_SMOOTH_UNIFORM)
@@ -2502,6 +2466,112 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
                      n_valid_out);
   HIP_TRY(hipGetLastError());
   return CCE_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Static scratch of cce_forward_noalloc: the forward's workspace for callers
+// that cannot allocate device memory.  Each device that runs the library holds
+// its own copy of this array (CCE_NOALLOC_SCRATCH_BYTES) until the process
+// ends.  In host code `scratch` names a host-side stand-in, not device memory:
+// the device address comes from hipGetSymbolAddress, once per device, and only
+// that address is passed to kernels.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[CCE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device and kept).
+int noalloc_scratch(void** out) {
+  int dev = -1;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(CCE_ERR_INVALID_ARG, "device ordinal %d outside [0, %d)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(CCE_ERR_HIP, "hipGetSymbolAddress(scratch) returned a null address on device %d", dev);
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return CCE_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+
+extern "C" {
+
+const char* cce_last_error(void) { return g_err; }
+
+int cce_abi_version(void) { return CCE_ABI_VERSION; }
+
+int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, int lse_rows, size_t* bytes) {
+  g_err[0] = 0;
+  if (!bytes) return fail(CCE_ERR_INVALID_ARG, "bytes must not be null");
+  int rc = check_dims(N, d, V);
+  if (rc) return rc;
+  if (reduction < CCE_REDUCTION_NONE || reduction > CCE_REDUCTION_SUM)
+    return fail(CCE_ERR_INVALID_ARG, "reduction must be 0 (none), 1 (mean) or 2 (sum), got %d", reduction);
+  if (lse_rows != CCE_LSE_ALL_ROWS && lse_rows != CCE_LSE_LABELLED_ROWS)
+    return fail(CCE_ERR_INVALID_ARG, "lse_rows must be CCE_LSE_ALL_ROWS or CCE_LSE_LABELLED_ROWS, got %d", lse_rows);
+  *bytes = fwd_layout(nullptr, N, d, V, reduction, lse_rows).bytes;
+  return CCE_OK;
+}
+
+int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_size, int need_grad_hidden,
+                                 int need_grad_weight, size_t* bytes) {
+  g_err[0] = 0;
+  if (!bytes) return fail(CCE_ERR_INVALID_ARG, "bytes must not be null");
+  int rc = check_dims(N, d, V);
+  if (rc) return rc;
+  *bytes = bwd_layout(nullptr, N, d, V, band_width(V, chunk_size, N, d), need_grad_hidden != 0, need_grad_weight != 0).bytes;
+  return CCE_OK;
+}
+
+int cce_forward(const void* hidden, const void* weight, const void* labels, int labels_int64, const float* bias,
+                int64_t N, int64_t d, int64_t V, int64_t ignore_index, float label_smoothing, float z_loss_weight,
+                int smoothing_form, int reduction, int lse_rows, float* loss_out, float* lse_out, float* target_out,
+                int32_t* n_valid_out, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  return forward_run(hidden, weight, labels, labels_int64, bias, N, d, V, ignore_index, label_smoothing,
+                     z_loss_weight, smoothing_form, reduction, lse_rows, loss_out, lse_out, target_out, n_valid_out,
+                     workspace, workspace_bytes, stream);
+}
+
+int cce_forward_noalloc(const void* hidden, const void* weight, const void* labels, int labels_int64,
+                        const float* bias, int64_t N, int64_t d, int64_t V, int64_t ignore_index,
+                        float label_smoothing, float z_loss_weight, int smoothing_form, int reduction, int lse_rows,
+                        float* loss_out, float* lse_out, float* target_out, int32_t* n_valid_out, void* stream) {
+  g_err[0] = 0;
+  int rc = check_dims(N, d, V);
+  if (rc) return rc;
+  if (reduction < CCE_REDUCTION_NONE || reduction > CCE_REDUCTION_SUM)
+    return fail(CCE_ERR_INVALID_ARG, "reduction must be 0 (none), 1 (mean) or 2 (sum), got %d", reduction);
+  if (lse_rows != CCE_LSE_ALL_ROWS && lse_rows != CCE_LSE_LABELLED_ROWS)
+    return fail(CCE_ERR_INVALID_ARG, "lse_rows must be CCE_LSE_ALL_ROWS or CCE_LSE_LABELLED_ROWS, got %d", lse_rows);
+  const size_t need = fwd_layout(nullptr, N, d, V, reduction, lse_rows).bytes;
+  if (need > (size_t)CCE_NOALLOC_SCRATCH_BYTES)
+    return fail(CCE_ERR_WORKSPACE,
+                "cce_forward_noalloc: this problem (N=%ld d=%ld V=%ld) needs %zu bytes of scratch, more than the "
+                "%zu-byte static scratch; call cce_forward with a workspace instead",
+                (long)N, (long)d, (long)V, need, (size_t)CCE_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  rc = noalloc_scratch(&ws);
+  if (rc) return rc;
+  return forward_run(hidden, weight, labels, labels_int64, bias, N, d, V, ignore_index, label_smoothing,
+                     z_loss_weight, smoothing_form, reduction, lse_rows, loss_out, lse_out, target_out, n_valid_out,
+                     ws, (size_t)CCE_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int cce_backward(const float* grad_out, const void* hidden, const void* weight, const void* labels, int labels_int64,

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define CCE_ABI_VERSION 4
+#define CCE_ABI_VERSION 5
 
 #define CCE_OK 0
 #define CCE_ERR_INVALID_ARG 1
@@ -106,6 +106,28 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
                 float label_smoothing, float z_loss_weight, int smoothing_form, int reduction, int lse_rows,
                 float* loss_out, float* lse_out, float* target_out, int32_t* n_valid_out,
                 void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * cce_forward without a workspace argument: the same computation and results
+ * (it runs cce_forward's kernels), with its scratch memory taken from a static
+ * device array of CCE_NOALLOC_SCRATCH_BYTES that the library holds on each
+ * device it runs on until the process ends.  No counterpart in the reference:
+ * it serves callers that cannot allocate device memory (work under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation); the call
+ * itself makes no device allocation and no allocating library call.
+ * Problems whose cce_forward_workspace_bytes exceeds
+ * CCE_NOALLOC_SCRATCH_BYTES return CCE_ERR_WORKSPACE.  `stream` must belong
+ * to the current device.  Every call on one device shares that device's
+ * array, so calls whose work overlaps on one device (concurrent streams, or
+ * host threads) race; calls ordered on one stream do not.  Nothing in the
+ * array needs to start at zero: every scratch value a call reads, the same
+ * call writes first.
+ */
+#define CCE_NOALLOC_SCRATCH_BYTES (64u << 20)
+int cce_forward_noalloc(const void* hidden, const void* weight, const void* labels, int labels_int64,
+                        const float* bias, int64_t N, int64_t d, int64_t V, int64_t ignore_index,
+                        float label_smoothing, float z_loss_weight, int smoothing_form, int reduction, int lse_rows,
+                        float* loss_out, float* lse_out, float* target_out, int32_t* n_valid_out, void* stream);
 
 /* Workspace bytes cce_backward needs (chunk_size = vocabulary band width). */
 int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_size,
