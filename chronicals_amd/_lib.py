@@ -11,7 +11,7 @@ import threading
 from . import build as _build
 
 # constants mirrored from include/chronicals_cce.h
-CCE_ABI_VERSION = 5
+CCE_ABI_VERSION = 6
 CCE_OK = 0
 CCE_ERR_INVALID_ARG = 1
 CCE_ERR_WORKSPACE = 2
@@ -56,7 +56,7 @@ SIGNATURES = {
     "cce_abi_version": (_i32, []),
     "cce_last_error": (ctypes.c_char_p, []),
     "cce_forward_workspace_bytes": (_i32, [_i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_sz)]),
-    "cce_backward_workspace_bytes": (_i32, [_i64, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_sz)]),
+    "cce_backward_workspace_bytes": (_i32, [_i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, ctypes.POINTER(_sz)]),
     "cce_forward": (_i32, [
         _vp, _vp, _vp, _i32, _vp,            # hidden, weight, labels, labels_int64, bias
         _i64, _i64, _i64, _i64,              # N, d, V, ignore_index
@@ -156,9 +156,12 @@ def forward_workspace_bytes(N: int, d: int, V: int, reduction: int, lse_rows: in
     return out.value
 
 
-def backward_workspace_bytes(N: int, d: int, V: int, chunk_size: int, need_dh: bool, need_dw: bool) -> int:
+def backward_workspace_bytes(N: int, d: int, V: int, chunk_size: int, need_dh: bool, need_dw: bool,
+                             dh_f32: bool = False, dw_f32: bool = False) -> int:
     out = _sz(0)
-    check(load().cce_backward_workspace_bytes(N, d, V, chunk_size, int(need_dh), int(need_dw), ctypes.byref(out)))
+    check(load().cce_backward_workspace_bytes(N, d, V, chunk_size, int(need_dh),
+                                              CCE_DTYPE_F32 if dh_f32 else CCE_DTYPE_BF16, int(need_dw),
+                                              CCE_DTYPE_F32 if dw_f32 else CCE_DTYPE_BF16, ctypes.byref(out)))
     return out.value
 
 

@@ -31,6 +31,7 @@
 #include <stddef.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 #include <math.h>
 #include <float.h>
@@ -214,9 +215,10 @@ struct LoaderSel<false, 256, W> {
 };
 
 // Row compaction: when `dyn` is set, `live` points at the device-side count
-// of live rows (a multiple of 256, or M).  kDynM: M is cut to it and the row
-// tiles past it do not run; kDynK: the reduction runs over the first `live`
-// rows only.
+// of live rows (a multiple of 256, or the row count), and the operand's rows
+// start at row live_base of that order (a block of rows), so the block holds
+// live - live_base of them.  kDynM: M is cut to that and the row tiles past
+// it do not run; kDynK: the reduction runs over those rows only.
 constexpr int kDynNone = 0, kDynM = 1, kDynK = 2;
 
 struct GemmShape {
@@ -227,7 +229,15 @@ struct GemmShape {
   int M, N, K;
   const int* live = nullptr;
   int dyn = kDynNone;
+  int live_base = 0;
+  // k offset of B in elements (direct-to-LDS pipelines): B's k index kb + k.
+  // The DMA's buffer range still ends where B's rows end, so a slab that runs
+  // past K reads the next row's (finite) values or zeros, never memory past B.
+  int kb = 0;
 };
+
+// Live rows of a row block that starts at row `base` of the compacted order.
+__device__ inline int live_rows(const int* live, int base) { return max(0, *live - base); }
 
 // Accumulator tile of one wave: kWaveRows rows x (BN/2) columns as
 // kFM x (BN/64) blocks of 32x32 fp32.
@@ -738,6 +748,7 @@ struct AccParams {
 // Plain GEMM output with optional fp32 accumulation buffer.
 //   mode 0: out = C            1: acc32 = C
 //   mode 2: acc32 += C          3: out = acc32 + C
+//   mode 4: out += C (fp32 output only: the output is its own accumulator)
 template <int BN, int W>
 struct EpiAcc {
   typedef AccParams Params;
@@ -772,14 +783,17 @@ struct EpiAcc {
         // before any add or store (one memory round trip per group, not per
         // 16-byte piece)
         f32x4 old[JG][4];
+        const long om = p.rowmap ? (long)p.rowmap[m] : (long)m;
         if (p.mode >= 2) {
+          // modes 2, 3 read the accumulator row m; mode 4 the output row om
+          const float* src = p.mode == 4 ? reinterpret_cast<const float*>(p.out) + om * p.ldo
+                                         : p.acc32 + (long)m * p.ldacc;
 #pragma unroll
           for (int jj = 0; jj < JG; ++jj)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
               const int n = tn * BN + acc_col<BN>(wn, j0 + jj, q, l);
-              old[jj][q] = n < g.N ? *reinterpret_cast<const f32x4*>(p.acc32 + (long)m * p.ldacc + n)
-                                   : f32x4{0.f, 0.f, 0.f, 0.f};
+              old[jj][q] = n < g.N ? *reinterpret_cast<const f32x4*>(src + n) : f32x4{0.f, 0.f, 0.f, 0.f};
             }
         }
 #pragma unroll
@@ -794,7 +808,6 @@ struct EpiAcc {
           if (p.mode == 1 || p.mode == 2) {
             *reinterpret_cast<f32x4*>(p.acc32 + (long)m * p.ldacc + n) = v;
           } else {
-            const long om = p.rowmap ? (long)p.rowmap[m] : (long)m;
             if (p.out_f32) {
               *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + om * p.ldo + n) = v;
             } else {
@@ -843,7 +856,7 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g_in, const typename 
   static_assert(PIPE >= 3 && PIPE <= 5, "pipelines: 3 (register-staged), 4 and 5 (direct-to-LDS)");
   typedef EpiT<BN, W> Epi;
   GemmShape g = g_in;
-  if (g.dyn == kDynK) g.K = min(g.K, *g.live);
+  if (g.dyn == kDynK) g.K = min(g.K, live_rows(g.live, g.live_base));
   if (g.dyn == kDynM) {
     // Only the row tiles below the live rows run.  Epilogues with
     // kDynSplits re-split the vocabulary over all nb workgroups themselves;
@@ -852,7 +865,7 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g_in, const typename 
     // row-dynamic launch), so that every XCD keeps an equal share, and the
     // remaining workgroups exit.
     const int gm = (g.M + kBM - 1) / kBM;
-    g.M = min(g.M, *g.live);
+    g.M = min(g.M, live_rows(g.live, g.live_base));
     if constexpr (!Epi::kDynSplits) {
       nb = nb / gm * ((g.M + kBM - 1) / kBM);
       if (bid >= nb) return;
@@ -911,7 +924,7 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g_in, const typename 
         dma_kmajor<kBM, W>(g.A, g.lda, a_r0, g.M, ik2 * kBK, S, w, l);
       else
         dma_mnmajor256<W>(g.A, g.lda, a_r0, ik2 * kBK, g.K, S, w, l);
-      dma_kmajor<BN, W>(g.B, g.ldb, it2 * BN, g.N, ik2 * kBK, S + kBM * 64, w, l);
+      dma_kmajor<BN, W>(g.B, g.ldb, it2 * BN, g.N, g.kb + ik2 * kBK, S + kBM * 64, w, l);
       if (++ik2 == KT) {
         ik2 = 0;
         ++it2;
@@ -1104,12 +1117,15 @@ __global__ __launch_bounds__(W * 64) void dual_acc_kernel(GemmShape g_dw, AccPar
 // partials P[k] = P + k * stride ([rows][d], GEMM row order) of each live row
 // are summed in fixed order and applied with the band's accumulator mode, as
 // the GEMM epilogue applies an unsplit tile: 0 out = s, 1 acc = s,
-// 2 acc += s, 3 out = acc + s; out rows go through the row map.  d % 64 == 0.
+// 2 acc += s, 3 out = acc + s, 4 out += s (fp32 out); out rows go through the
+// row map.  The rows are a block starting at row live_base of the compacted
+// order (P, acc and rowmap point at the block).  d % 64 == 0.
 struct DhReduce {
   const float* P;
   long stride;
   int ks, N, d;
   const int* live;
+  int live_base;
   float* acc;
   int mode;
   void* out;
@@ -1119,7 +1135,7 @@ struct DhReduce {
 
 // Items (row, 4 columns) first, first + step, ... of a DhReduce.
 __device__ inline void dh_reduce_body(const DhReduce& r, long first, long step) {
-  const int rows = r.live ? min(r.live[0], r.N) : r.N;
+  const int rows = r.live ? min(live_rows(r.live, r.live_base), r.N) : r.N;
   const int q = r.d >> 2;
   const long total = (long)rows * q;
   for (long i = first; i < total; i += step) {
@@ -1134,6 +1150,7 @@ __device__ inline void dh_reduce_body(const DhReduce& r, long first, long step) 
     }
     if (r.mode == 3) s = *reinterpret_cast<const f32x4*>(r.acc + o) + s;
     const long oo = (long)(r.rowmap ? r.rowmap[m] : m) * r.d + (i % q) * 4;
+    if (r.mode == 4) s = *reinterpret_cast<const f32x4*>(static_cast<const float*>(r.out) + oo) + s;
     if (r.out_f32)
       *reinterpret_cast<f32x4*>(static_cast<float*>(r.out) + oo) = s;
     else
@@ -1918,12 +1935,14 @@ __global__ __launch_bounds__(256) void transpose_kernel(const bf16_t* __restrict
 }
 
 // dB[c] = sum_m G[m][c] for c < C (fixed order: deterministic).  Block = 64
-// columns.  With `live`, M = min(M, live[0]).
+// columns.  With `live`, M = min(M, live rows of the block at live_base);
+// with `accumulate`, out[c] += the sum (row blocks after the first).
 __global__ __launch_bounds__(256) void colsum_kernel(const bf16_t* __restrict__ G, long ldg, int M, int C,
-                                                     const int* __restrict__ live, float* __restrict__ out) {
+                                                     const int* __restrict__ live, int live_base, int accumulate,
+                                                     float* __restrict__ out) {
   // blockIdx.y = row split: rows [y*M/gridDim.y, (y+1)*M/gridDim.y) into out[y][C]
   __shared__ float part[32][65];
-  if (live) M = min(M, live[0]);
+  if (live) M = min(M, live_rows(live, live_base));
   const int tid = threadIdx.x;
   const int cg = tid & 7, rg = tid >> 3;  // 8 column groups of 8, 32 row groups
   const int c0 = blockIdx.x * 64 + cg * 8;
@@ -1949,7 +1968,7 @@ __global__ __launch_bounds__(256) void colsum_kernel(const bf16_t* __restrict__ 
     float s = 0.f;
     for (int r = 0; r < 32; ++r) s += part[r][tid];
     const int c = blockIdx.x * 64 + tid;
-    if (c < C) out[c] = s;
+    if (c < C) out[c] = accumulate ? out[c] + s : s;
   }
 }
 
@@ -2042,24 +2061,51 @@ int forward_splits(long N, long d, long V, bool compact) {
   return (int)s;
 }
 
-// Vocabulary band width: chunk rounded up to a multiple of 256, within
-// [256, V rounded up] and at most 2^20 columns (a band's 256-row operand
-// tiles then stay inside one buffer descriptor's 2 GB range).
+// Vocabulary band width: chunk rounded up to a multiple of 256, at most
+// kBandCap (8192) columns and at least 256, within V rounded up.  chunk_size
+// bounds the band from above only: the reference's trainer asks for 16384 at
+// V >= 128K (get_optimal_chunk_size), which here would double the band
+// buffers for no measured gain.
 constexpr long kMaxBand = 1L << 20;
+constexpr long kBandCap = 8192;
 long band_width(long V, long chunk, long N, long d) {
-  long vb = chunk <= 0 ? 8192 : (chunk > kMaxBand ? kMaxBand : chunk);
+  long vb = chunk <= 0 ? kBandCap : std::min(chunk, kBandCap);
   vb = align_up((size_t)vb, 256);
   // with few rows a band launch is short and its fixed costs dominate: up to
   // 4x wider bands, while the band buffers (G: rows x band, W^T: d x band)
-  // stay within what 4096 rows take at chunk_size.  Below 1024 rows W^T and
+  // stay within what 4096 rows take at that band.  Below 1024 rows W^T and
   // the dH partials would outgrow the logits themselves, for no measured gain.
   const long rows = (long)align_up((size_t)(N > 0 ? N : 1), 256);
   const long f = rows < 1024 ? 1 : std::min<long>(4, std::max<long>(1, (4096 + d) / (rows + d)));
-  vb = std::min<long>(vb * f, std::max<long>(vb, kMaxBand / 256 * 256));
+  vb = std::min<long>(vb * f, kMaxBand);
   const long vmax = (long)align_up((size_t)V, 256);
   if (vb > vmax) vb = vmax;
   if (vb < 256) vb = 256;
   return vb;
+}
+
+// Rows per block of the backward.  The band gradient G of a block is
+// (rows x band) bf16 and there are two such buffers (band b+1's recompute
+// overlaps band b's GEMMs), so a block has at most budget / (4 * band) rows,
+// a multiple of 256; a batch that fits is one block.  G's memory is then
+// bounded by the budget whatever N is; dW of a band accumulates over the
+// blocks.  The budget is 512 MiB, or CHRONICALS_CCE_G_BUDGET_MB from the
+// environment (read on every call, so a workspace query and the call it
+// sizes must see the same value).
+constexpr long kGBudget = 512L << 20;
+long g_budget() {
+  const char* e = getenv("CHRONICALS_CCE_G_BUDGET_MB");
+  if (e && *e) {
+    const long mb = strtol(e, nullptr, 10);
+    if (mb > 0 && mb < (1L << 20)) return mb << 20;
+  }
+  return kGBudget;
+}
+long block_rows(long N, long Vb) {
+  const long n = std::max<long>(N, 1);
+  long nb = g_budget() / (4 * Vb) / kBM * kBM;
+  if (nb < kBM) nb = kBM;
+  return nb >= n ? n : nb;
 }
 
 struct FwdLayout {
@@ -2113,18 +2159,22 @@ FwdLayout fwd_layout(void* ws, long N, long d, long V, int reduction, int lse_ro
 }
 
 struct BwdLayout {
+  long Vb, Nb;    // band width, rows per block
+  int nblocks;    // row blocks
   float4* rowp;
   int* rowlab;
-  bf16_t* G[2];   // band gradient buffers; the second only when bands alternate
+  bf16_t* G[2];   // band gradient of a block; the second only when units alternate
   bf16_t* WT[2];  // W band transposes; the second only when bands alternate
   bf16_t* HT;
-  float* dHacc;
+  float* dHacc;   // dH over the bands (bf16 dH with several bands; fp32 dH accumulates in place)
+  float* dWacc;   // dW of a band over the row blocks (bf16 dW with several blocks)
   // row compaction (banded backward): row order, live row count, H in that order
   int* idx;
   int* live;
   bf16_t* Hc;
-  // fp32 partials of a K-split dH: dh_ks slices of [N][d] per band, in two
-  // alternating buffers when there are several bands; null when unsplit
+  // fp32 partials of a K-split dH: dh_ks slices of [Nb][d] per unit, in two
+  // alternating buffers when the reduction is folded into the next launch;
+  // null when unsplit
   float* dhpart;
   int dh_ks;
   size_t bytes;
@@ -2138,17 +2188,17 @@ bool banded(long d) { return d % 64 == 0; }
 // when d % 256 <= 128, is one 128-wide tail tile.
 long band_dmain(long d) { return (d % 256 == 0 || d % 256 > 128) ? d : d - d % 256; }
 
+// With 4 or more K splits (very few rows) the band launches are short, and
+// each band's dH reduction rides in the next band's launch (two partial
+// buffers, alternating); with 2-3 splits it is a launch of its own.
+bool dh_fold(int ks) { return ks >= 4; }
+
 // K splits of the banded dH.  dH has one tile per (256-row tile, hidden
 // column tile), each reducing over the whole band; with few rows those tiles
 // cannot fill the CUs and the band launch waits on their long K loops.  Then
 // K is split so that tiles x splits reaches about 128 workgroups, with at
 // least 8 slabs of 64 per split (more splits cost more in the fp32 partials'
 // reduction than their shorter K loops return).
-// With 4 or more K splits (very few rows) the band launches are short, and
-// each band's dH reduction rides in the next band's launch (two partial
-// buffers, alternating); with 2-3 splits it is a launch of its own.
-bool dh_fold(int ks) { return ks >= 4; }
-
 int dh_splits(long N, long d, long Vb) {
   if (!banded(d) || N <= 0 || d <= 0) return 1;
   const long dmain = band_dmain(d);
@@ -2158,28 +2208,34 @@ int dh_splits(long N, long d, long Vb) {
   return ks < 2 ? 1 : (int)ks;
 }
 
-BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bool need_dw) {
+BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bool need_dw, bool dh_f32,
+                     bool dw_f32) {
   Carver c(ws);
   BwdLayout L;
+  L.Vb = Vb;
+  L.Nb = block_rows(N, Vb);
+  L.nblocks = (int)ceil_div(std::max<long>(N, 1), L.Nb);
   const long nbands = ceil_div(V, Vb);
+  const long units = nbands * L.nblocks;
   const long N8 = (long)align_up((size_t)N, 8);
   L.rowp = c.take<float4>((size_t)N);
   L.rowlab = c.take<int>((size_t)N);
-  L.G[0] = c.take<bf16_t>((size_t)N * Vb);
-  L.G[1] = (banded(d) && nbands > 1) ? c.take<bf16_t>((size_t)N * Vb) : L.G[0];
+  L.G[0] = c.take<bf16_t>((size_t)L.Nb * Vb);
+  L.G[1] = (banded(d) && units > 1) ? c.take<bf16_t>((size_t)L.Nb * Vb) : L.G[0];
   L.WT[0] = need_dh ? c.take<bf16_t>((size_t)d * Vb) : nullptr;
   L.WT[1] = (need_dh && banded(d) && nbands > 1) ? c.take<bf16_t>((size_t)d * Vb) : L.WT[0];
   L.HT = need_dw ? c.take<bf16_t>((size_t)d * N8) : nullptr;
-  L.dHacc = (need_dh && nbands > 1) ? c.take<float>((size_t)N * d) : nullptr;
+  L.dHacc = (need_dh && nbands > 1 && !dh_f32) ? c.take<float>((size_t)N * d) : nullptr;
+  L.dWacc = (need_dw && L.nblocks > 1 && !dw_f32) ? c.take<float>((size_t)Vb * d) : nullptr;
   const bool compact = banded(d);
   L.idx = compact ? c.take<int>((size_t)N) : nullptr;
   L.live = compact ? c.take<int>(1) : nullptr;
   L.Hc = compact ? c.take<bf16_t>((size_t)N * d) : nullptr;
-  L.dh_ks = need_dh ? dh_splits(N, d, Vb) : 1;
-  // a second partial buffer only when the reduction rides in the next band's
-  // launch (dh_fold); otherwise each band's reduction runs before the next
+  L.dh_ks = need_dh ? dh_splits(L.Nb, d, Vb) : 1;
+  // a second partial buffer only when the reduction rides in the next
+  // launch (dh_fold); otherwise each unit's reduction runs before the next
   // band launch writes the one buffer again
-  L.dhpart = L.dh_ks > 1 ? c.take<float>((size_t)(dh_fold(L.dh_ks) && nbands > 1 ? 2 : 1) * L.dh_ks * N * d)
+  L.dhpart = L.dh_ks > 1 ? c.take<float>((size_t)(dh_fold(L.dh_ks) && units > 1 ? 2 : 1) * L.dh_ks * L.Nb * d)
                          : nullptr;
   L.bytes = align_up(c.off, 256);
   return L;
@@ -2298,18 +2354,19 @@ int launch_acc(const GemmShape& g, const AccParams& ep, hipStream_t st, int kind
   return launch_gemm<BN, kWarp8, AK, true, EpiAcc, PIPE>(g, ep, nb, st, kind, true);
 }
 
-// Recompute launch shape of one band: G[n][c] for columns [v0, v0 + vb).
+// Recompute launch shape of one unit: G[n][c] for the rows [m0, m0 + rows)
+// of the compacted order (a row block) and columns [v0, v0 + vb).
 // A recompute launch of its own runs each workgroup over a run of column
 // tiles (about CCE_GRAD_WGS workgroups: fewer pipeline restarts); inside the
 // band launch (`in_band`) each workgroup takes one tile, the finest grain for
 // filling the CUs that the long dW / dH tiles leave idle.
-void grad_shape(const bf16_t* H, const bf16_t* W, const float* bias, const BwdLayout& L, bf16_t* G, long N, long d,
-                long Vb, long v0, long vb, int bn, bool in_band, GemmShape& g, GradParams& e, int& nb) {
-  const int gm = (int)ceil_div(N, kBM);
-  g.A = L.Hc ? L.Hc : H; g.lda = d; g.B = W + v0 * d; g.ldb = d;
-  g.M = (int)N; g.N = (int)vb; g.K = (int)d;
-  g.live = L.live; g.dyn = L.live ? kDynM : kDynNone;
-  e.bias = bias; e.rowp = L.rowp; e.rowlab = L.rowlab; e.G = G; e.ldg = Vb; e.v0 = (int)v0;
+void grad_shape(const bf16_t* H, const bf16_t* W, const float* bias, const BwdLayout& L, bf16_t* G, long m0,
+                long rows, long d, long v0, long vb, int bn, bool in_band, GemmShape& g, GradParams& e, int& nb) {
+  const int gm = (int)ceil_div(rows, kBM);
+  g.A = (L.Hc ? L.Hc : H) + m0 * d; g.lda = d; g.B = W + v0 * d; g.ldb = d;
+  g.M = (int)rows; g.N = (int)vb; g.K = (int)d;
+  g.live = L.live; g.dyn = L.live ? kDynM : kDynNone; g.live_base = (int)m0;
+  e.bias = bias; e.rowp = L.rowp + m0; e.rowlab = L.rowlab + m0; e.G = G; e.ldg = L.Vb; e.v0 = (int)v0;
   e.tiles_n = (int)ceil_div(vb, bn);
   e.splits = in_band ? e.tiles_n : (int)std::min<long>(e.tiles_n, std::max<long>(1, ceil_div(CCE_GRAD_WGS, gm)));
   nb = gm * e.splits;
@@ -2447,7 +2504,7 @@ int forward_run(const void* hidden, const void* weight, const void* labels, int 
   const bool uniform = smoothing_form == CCE_SMOOTH_UNIFORM && label_smoothing > 0.f;
   if (uniform) {
     hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)ceil_div(d, 64), (unsigned)L.wsplits), dim3(256), 0, st,
-                       static_cast<const bf16_t*>(weight), (long)d, (int)V, (int)d, nullptr, L.wpart);
+                       static_cast<const bf16_t*>(weight), (long)d, (int)V, (int)d, nullptr, 0, 0, L.wpart);
     HIP_TRY(hipGetLastError());
     hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)ceil_div(d, 256)), dim3(256), 0, st, L.wpart, L.wsplits,
                        (int)d, bias, (int)V, L.wsum);
@@ -2530,12 +2587,17 @@ int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, 
 }
 
 int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_size, int need_grad_hidden,
-                                 int need_grad_weight, size_t* bytes) {
+                                 int grad_hidden_dtype, int need_grad_weight, int grad_weight_dtype, size_t* bytes) {
   g_err[0] = 0;
   if (!bytes) return fail(CCE_ERR_INVALID_ARG, "bytes must not be null");
   int rc = check_dims(N, d, V);
   if (rc) return rc;
-  *bytes = bwd_layout(nullptr, N, d, V, band_width(V, chunk_size, N, d), need_grad_hidden != 0, need_grad_weight != 0).bytes;
+  if ((need_grad_hidden && grad_hidden_dtype != CCE_DTYPE_BF16 && grad_hidden_dtype != CCE_DTYPE_F32) ||
+      (need_grad_weight && grad_weight_dtype != CCE_DTYPE_BF16 && grad_weight_dtype != CCE_DTYPE_F32))
+    return fail(CCE_ERR_INVALID_ARG, "gradient dtypes must be CCE_DTYPE_BF16 or CCE_DTYPE_F32");
+  *bytes = bwd_layout(nullptr, N, d, V, band_width(V, chunk_size, N, d), need_grad_hidden != 0,
+                      need_grad_weight != 0, grad_hidden_dtype == CCE_DTYPE_F32,
+                      grad_weight_dtype == CCE_DTYPE_F32).bytes;
   return CCE_OK;
 }
 
@@ -2597,20 +2659,21 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
   const bool need_dh = grad_hidden != nullptr, need_dw = grad_weight != nullptr, need_db = grad_bias != nullptr;
   if (need_db && !bias) return fail(CCE_ERR_INVALID_ARG, "grad_bias requested without bias");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool dh_f32 = grad_hidden_dtype == CCE_DTYPE_F32, dw_f32 = grad_weight_dtype == CCE_DTYPE_F32;
   const long Vb = band_width(V, chunk_size, N, d);
-  const BwdLayout need = bwd_layout(nullptr, N, d, V, Vb, need_dh, need_dw);
+  const BwdLayout need = bwd_layout(nullptr, N, d, V, Vb, need_dh, need_dw, dh_f32, dw_f32);
   if (workspace_bytes < need.bytes || (need.bytes && !workspace))
     return fail(CCE_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need.bytes, workspace_bytes);
   if (N == 0) {
     if (need_dw) {
-      rc = zero_fill(grad_weight, (size_t)V * d * (grad_weight_dtype == CCE_DTYPE_F32 ? 4 : 2), st);
+      rc = zero_fill(grad_weight, (size_t)V * d * (dw_f32 ? 4 : 2), st);
       if (rc) return rc;
     }
     if (need_db) return zero_fill(grad_bias, (size_t)V * 4, st);
     return CCE_OK;
   }
   if (!need_dh && !need_dw && !need_db) return CCE_OK;
-  const BwdLayout L = bwd_layout(workspace, N, d, V, Vb, need_dh, need_dw);
+  const BwdLayout L = bwd_layout(workspace, N, d, V, Vb, need_dh, need_dw, dh_f32, dw_f32);
   const long N8 = (long)align_up((size_t)N, 8);
   const bf16_t* H = static_cast<const bf16_t*>(hidden);
   const bf16_t* W = static_cast<const bf16_t*>(weight);
@@ -2626,7 +2689,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
                        st, H, (int)d, L.idx, (int)N, L.Hc);
     HIP_TRY(hipGetLastError());
     if (need_dh) {
-      const long row_bytes = d * (grad_hidden_dtype == CCE_DTYPE_F32 ? 4 : 2);
+      const long row_bytes = d * (dh_f32 ? 4 : 2);
       hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)std::min<long>(ceil_div(N * (row_bytes / 16), 256), 4096)),
                          dim3(256), 0, st, static_cast<char*>(grad_hidden), row_bytes, L.idx, L.live, (int)N);
       HIP_TRY(hipGetLastError());
@@ -2642,11 +2705,16 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     HIP_TRY(hipGetLastError());
   }
 
+  // Work units (b, r): vocabulary band b, row block r (rows [r*Nb, r*Nb +
+  // Nb) of the compacted order), band-major.  Each unit's gradient block G
+  // (rows x band) lives in G[u & 1] for unit u = b * nblocks + r.
   const long nbands = ceil_div(V, Vb);
-  const int gm = (int)ceil_div(N, kBM);
+  const int R = L.nblocks;
+  const long Nb = L.Nb;
+  const long units = nbands * R;
   // The partial band (V - (nbands - 1) * Vb columns) comes first: its logits
   // recompute then runs alone, where it is shortest, and the last launch,
-  // which has no next band's recompute to fill the CUs its long dW tiles
+  // which has no next unit's recompute to fill the CUs its long dW tiles
   // leave idle, gets a full band.
   const long head = V - (nbands - 1) * Vb;
   auto band_cols = [&](long b, long& v0, long& vb, long& vb64) {
@@ -2654,41 +2722,63 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     vb = b == 0 ? head : Vb;
     vb64 = (long)align_up((size_t)vb, 64);
   };
-  // dH of one band: G[N][vb64] . WT[d][vb64]^T over hidden columns [c0, c0 + nc)
-  auto dh_shape = [&](long b, const bf16_t* G, long c0, long nc, GemmShape& g, AccParams& e) {
-    long v0, vb, vb64;
-    band_cols(b, v0, vb, vb64);
-    g.A = G; g.lda = Vb; g.B = L.WT[b & 1] + c0 * Vb; g.ldb = Vb;
-    g.M = (int)N; g.N = (int)nc; g.K = (int)vb64;
-    g.live = L.live; g.dyn = L.live ? kDynM : kDynNone;
-    e.rowmap = L.idx;
-    e.acc32 = L.dHacc ? L.dHacc + c0 : nullptr; e.ldacc = d;
-    e.out = (grad_hidden_dtype == CCE_DTYPE_F32) ? static_cast<void*>(static_cast<float*>(grad_hidden) + c0)
-                                                 : static_cast<void*>(static_cast<bf16_t*>(grad_hidden) + c0);
-    e.ldo = d;
-    e.out_f32 = (grad_hidden_dtype == CCE_DTYPE_F32);
-    e.mode = (nbands == 1) ? 0 : (b == 0 ? 1 : (b == nbands - 1 ? 3 : 2));
+  auto block_span = [&](long r, long& m0, long& rows) {
+    m0 = r * Nb;
+    rows = std::min<long>(Nb, N - m0);
   };
-  // dW of one band: rows [v0, v0 + vb), hidden columns [c0, c0 + nc) of
-  // grad_weight = G^T . H
-  auto dw_shape = [&](long b, const bf16_t* G, long c0, long nc, GemmShape& g, AccParams& e) {
-    long v0, vb, vb64;
+  // dH accumulates over the bands: the first band stores, middle bands add,
+  // the last writes the output (fp32 dH: the output is the accumulator)
+  auto dh_mode = [&](long b) {
+    if (nbands == 1) return 0;
+    if (dh_f32) return b == 0 ? 0 : 4;
+    return b == 0 ? 1 : (b == nbands - 1 ? 3 : 2);
+  };
+  // dW of a band accumulates over the row blocks in the same way
+  auto dw_mode = [&](long r) {
+    if (R == 1) return 0;
+    if (dw_f32) return r == 0 ? 0 : 4;
+    return r == 0 ? 1 : (r == R - 1 ? 3 : 2);
+  };
+  // dH of unit (b, r): G[rows][vb64] . WT[d][vb64]^T over hidden columns [c0, c0 + nc)
+  auto dh_shape = [&](long b, long r, const bf16_t* G, long c0, long nc, GemmShape& g, AccParams& e) {
+    long v0, vb, vb64, m0, rows;
     band_cols(b, v0, vb, vb64);
-    g.A = G; g.lda = Vb;  // MN-major: element (v, n) at G[n*Vb + v]
-    g.B = L.HT + c0 * N8; g.ldb = N8;
-    g.M = (int)vb; g.N = (int)nc; g.K = (int)N;
-    g.live = L.live; g.dyn = L.live ? kDynK : kDynNone;
-    e.rowmap = nullptr;
-    e.acc32 = nullptr; e.ldacc = 0;
-    const long o = v0 * d + c0;
-    e.out = (grad_weight_dtype == CCE_DTYPE_F32) ? static_cast<void*>(static_cast<float*>(grad_weight) + o)
-                                                 : static_cast<void*>(static_cast<bf16_t*>(grad_weight) + o);
+    block_span(r, m0, rows);
+    g.A = G; g.lda = Vb; g.B = L.WT[b & 1] + c0 * Vb; g.ldb = Vb;
+    g.M = (int)rows; g.N = (int)nc; g.K = (int)vb64;
+    g.live = L.live; g.dyn = L.live ? kDynM : kDynNone; g.live_base = (int)m0;
+    e.rowmap = L.idx ? L.idx + m0 : nullptr;
+    e.acc32 = L.dHacc ? L.dHacc + m0 * d + c0 : nullptr; e.ldacc = d;
+    // with a row map the output rows are global (the map holds them);
+    // without one (no compaction) the block's rows start at m0
+    const long orow = L.idx ? 0 : m0;
+    e.out = dh_f32 ? static_cast<void*>(static_cast<float*>(grad_hidden) + orow * d + c0)
+                   : static_cast<void*>(static_cast<bf16_t*>(grad_hidden) + orow * d + c0);
     e.ldo = d;
-    e.out_f32 = (grad_weight_dtype == CCE_DTYPE_F32);
-    e.mode = 0;
+    e.out_f32 = dh_f32;
+    e.mode = dh_mode(b);
+  };
+  // dW of unit (b, r): rows [v0, v0 + vb), hidden columns [c0, c0 + nc) of
+  // grad_weight = G^T . H over the block's rows
+  auto dw_shape = [&](long b, long r, const bf16_t* G, long c0, long nc, GemmShape& g, AccParams& e) {
+    long v0, vb, vb64, m0, rows;
+    band_cols(b, v0, vb, vb64);
+    block_span(r, m0, rows);
+    g.A = G; g.lda = Vb;  // MN-major: element (v, n) at G[n*Vb + v]
+    g.B = L.HT + c0 * N8; g.ldb = N8; g.kb = (int)m0;  // H^T columns [m0, m0 + rows)
+    g.M = (int)vb; g.N = (int)nc; g.K = (int)rows;
+    g.live = L.live; g.dyn = L.live ? kDynK : kDynNone; g.live_base = (int)m0;
+    e.rowmap = nullptr;
+    e.acc32 = L.dWacc ? L.dWacc + c0 : nullptr; e.ldacc = d;
+    const long o = v0 * d + c0;
+    e.out = dw_f32 ? static_cast<void*>(static_cast<float*>(grad_weight) + o)
+                   : static_cast<void*>(static_cast<bf16_t*>(grad_weight) + o);
+    e.ldo = d;
+    e.out_f32 = dw_f32;
+    e.mode = dw_mode(r);
   };
   // WT[b & 1][j][c] = W[v0 + c][j], zero for vb <= c < vb64: as its own
-  // launch, or as the transpose population of the previous band's launch
+  // launch, or as the transpose population of an earlier launch
   auto transpose_params = [&](long b, TransposeParams& t) -> int {
     long v0, vb, vb64;
     band_cols(b, v0, vb, vb64);
@@ -2705,26 +2795,32 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     HIP_TRY(hipGetLastError());
     return CCE_OK;
   };
-  auto colsum_band = [&](long b, const bf16_t* G) -> int {
-    long v0, vb, vb64;
+  // dB[v0 .. v0 + vb) = sum over the block's rows of G, added over the blocks
+  auto colsum_unit = [&](long b, long r, const bf16_t* G) -> int {
+    long v0, vb, vb64, m0, rows;
     band_cols(b, v0, vb, vb64);
-    hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)ceil_div(vb, 64)), dim3(256), 0, st, G, (long)Vb, (int)N,
-                       (int)vb, L.live, grad_bias + v0);
+    block_span(r, m0, rows);
+    hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)ceil_div(vb, 64)), dim3(256), 0, st, G, (long)Vb, (int)rows,
+                       (int)vb, L.live, (int)m0, r > 0 ? 1 : 0, grad_bias + v0);
     HIP_TRY(hipGetLastError());
     return CCE_OK;
   };
+  auto grad_unit = [&](long u, bool in_band, int bn, GemmShape& g, GradParams& e, int& nb) {
+    long v0, vb, vb64, m0, rows;
+    band_cols(u / R, v0, vb, vb64);
+    block_span(u % R, m0, rows);
+    grad_shape(H, W, bias, L, L.G[u & 1], m0, rows, d, v0, vb, bn, in_band, g, e, nb);
+  };
 
   if (banded(d)) {
-    // launch b: dW(b), dH(b) from G[b & 1] and the recompute of band b+1 into
-    // G[(b+1) & 1]; band 0's recompute runs alone first.
+    // launch u: dW and dH of unit u from G[u & 1] and the recompute of unit
+    // u+1 into G[(u+1) & 1]; unit 0's recompute runs alone first.
     const long dmain = band_dmain(d);
     {
-      long v0, vb, vb64;
-      band_cols(0, v0, vb, vb64);
       GemmShape g1 = {};
       GradParams e1 = {};
       int nb1 = 0;
-      grad_shape(H, W, bias, L, L.G[0], N, d, Vb, v0, vb, kFastBN, false, g1, e1, nb1);
+      grad_unit(0, false, kFastBN, g1, e1, nb1);
       rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiGradBias, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false)
                 : launch_gemm<kFastBN, kWarp8, true, true, EpiGrad, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false);
       if (rc) return rc;
@@ -2733,44 +2829,55 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
         if (rc) return rc;
       }
     }
-    // the reduction of band b's K-split dH partials, with that band's
-    // accumulator mode (as dh_shape sets it)
     // With 4 or more splits (very few rows) the band launches are short and the
-    // reduction rides in the next band's launch, so the partials alternate
-    // between two buffers; with 2-3 splits the launches are full and it runs
-    // as a launch of its own after each band, on the one buffer.
+    // reduction rides in the next launch, so the partials alternate between
+    // two buffers; with 2-3 splits the launches are full and it runs as a
+    // launch of its own after each unit, on the one buffer.
     const bool fold = L.dhpart && dh_fold(L.dh_ks);
-    auto dh_part = [&](long b) { return L.dhpart + (fold ? (b & 1) : 0) * (long)L.dh_ks * N * d; };
-    auto dh_reduction = [&](long b, int ks) {
+    auto dh_part = [&](long u) { return L.dhpart + (fold ? (u & 1) : 0) * (long)L.dh_ks * Nb * d; };
+    // the reduction of unit u's K-split dH partials, with its band's
+    // accumulator mode (as dh_shape sets it)
+    auto dh_reduction = [&](long u, int ks) {
+      const long b = u / R;
+      long m0, rows;
+      block_span(u % R, m0, rows);
       DhReduce r;
-      r.P = dh_part(b);
-      r.stride = N * d;
-      r.ks = ks; r.N = (int)N; r.d = (int)d;
-      r.live = L.live;
-      r.acc = L.dHacc;
-      r.mode = (nbands == 1) ? 0 : (b == 0 ? 1 : (b == nbands - 1 ? 3 : 2));
-      r.out = grad_hidden;
-      r.out_f32 = (grad_hidden_dtype == CCE_DTYPE_F32);
-      r.rowmap = L.idx;
+      r.P = dh_part(u);
+      r.stride = Nb * d;
+      r.ks = ks; r.N = (int)rows; r.d = (int)d;
+      r.live = L.live; r.live_base = (int)m0;
+      r.acc = L.dHacc ? L.dHacc + m0 * d : nullptr;
+      r.mode = dh_mode(b);
+      r.out = L.idx ? grad_hidden
+                    : (dh_f32 ? static_cast<void*>(static_cast<float*>(grad_hidden) + m0 * d)
+                              : static_cast<void*>(static_cast<bf16_t*>(grad_hidden) + m0 * d));
+      r.out_f32 = dh_f32;
+      r.rowmap = L.idx ? L.idx + m0 : nullptr;
       return r;
     };
     int prev_ks = 1;
-    for (long b = 0; b < nbands; ++b) {
-      const bf16_t* G = L.G[b & 1];
+    for (long u = 0; u < units; ++u) {
+      const long b = u / R, r = u % R;
+      const bf16_t* G = L.G[u & 1];
       BandLaunch p = {};
       if (need_dw) {
         if (dmain > 0) {
-          dw_shape(b, G, 0, dmain, p.dw, p.e_dw);
+          dw_shape(b, r, G, 0, dmain, p.dw, p.e_dw);
           p.nb_dw = (int)(ceil_div(p.dw.M, kBM) * ceil_div(dmain, kFastBN));
         }
         if (dmain < d) {
-          dw_shape(b, G, dmain, d - dmain, p.dw2, p.e_dw2);
+          dw_shape(b, r, G, dmain, d - dmain, p.dw2, p.e_dw2);
           p.nb_dw2 = (int)(ceil_div(p.dw2.M, kBM) * ceil_div(d - dmain, kSlowBN));
         }
       }
       if (need_dh) {
-        if (b + 1 < nbands) p.nb_tr = transpose_params(b + 1, p.tr);  // into the other WT buffer
-        // K splits of this band: every split non-empty and a whole number of slabs
+        // the next band's W rows, transposed into the other WT buffer by the
+        // band's first launch (band b reads WT[b & 1] in all its launches)
+        if (r == 0 && b + 1 < nbands) p.nb_tr = transpose_params(b + 1, p.tr);
+        long m0, rows;
+        block_span(r, m0, rows);
+        const int gm = (int)ceil_div(rows, kBM);
+        // K splits of this unit: every split non-empty and a whole number of slabs
         int ks = 1;
         if (L.dhpart) {
           long v0, vb, vb64;
@@ -2778,71 +2885,77 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
           p.dh_kc = (int)align_up((size_t)ceil_div(vb64, L.dh_ks), 64);
           ks = (int)ceil_div(vb64, p.dh_kc);
         }
-        p.dh_split = L.dhpart != nullptr;  // every band, even one left with a single split
+        p.dh_split = L.dhpart != nullptr;  // every unit, even one left with a single split
         p.dh_ks = ks;
-        p.dh_part_stride = N * d;
-        float* const part = L.dhpart ? dh_part(b) : nullptr;
+        p.dh_part_stride = Nb * d;
+        float* const part = L.dhpart ? dh_part(u) : nullptr;
         if (dmain > 0) {
-          dh_shape(b, G, 0, dmain, p.dh, p.e_dh);
+          dh_shape(b, r, G, 0, dmain, p.dh, p.e_dh);
           p.nb_dh = gm * (int)ceil_div(dmain, kFastBN) * ks;
           p.e_dh_part = p.e_dh;
           p.e_dh_part.acc32 = part; p.e_dh_part.ldacc = d; p.e_dh_part.mode = 1; p.e_dh_part.rowmap = nullptr;
         }
         if (dmain < d) {
-          dh_shape(b, G, dmain, d - dmain, p.dh2, p.e_dh2);
+          dh_shape(b, r, G, dmain, d - dmain, p.dh2, p.e_dh2);
           p.nb_dh2 = gm * (int)ceil_div(d - dmain, kSlowBN) * ks;
           p.e_dh2_part = p.e_dh2;
           p.e_dh2_part.acc32 = part ? part + dmain : nullptr; p.e_dh2_part.ldacc = d;
           p.e_dh2_part.mode = 1; p.e_dh2_part.rowmap = nullptr;
         }
-        // the previous band's partials (the other buffer) into the accumulator
-        if (fold && b > 0) {
-          p.red = dh_reduction(b - 1, prev_ks);
-          p.nb_red = (int)std::min<long>(ceil_div(N * (d / 4), kWarp8 * 64 * 4), 1024);
+        // the previous unit's partials (the other buffer) into the accumulator
+        if (fold && u > 0) {
+          p.red = dh_reduction(u - 1, prev_ks);
+          long pm0, prows;
+          block_span((u - 1) % R, pm0, prows);
+          p.nb_red = (int)std::min<long>(ceil_div(prows * (d / 4), kWarp8 * 64 * 4), 1024);
         }
         prev_ks = ks;
       }
-      if (b + 1 < nbands) {
-        long v0, vb, vb64;
-        band_cols(b + 1, v0, vb, vb64);
-        grad_shape(H, W, bias, L, L.G[(b + 1) & 1], N, d, Vb, v0, vb, kFastBN, true, p.gr, p.e_gr, p.nb_gr);
-      }
+      if (u + 1 < units) grad_unit(u + 1, true, kFastBN, p.gr, p.e_gr, p.nb_gr);
       rc = launch_band(p, bias != nullptr, st);
       if (rc) return rc;
-      if (need_dh && L.dhpart && (!fold || b + 1 == nbands)) {
-        // this band's partials (the last band's go to the output: mode 0 or 3)
-        hipLaunchKernelGGL(dh_reduce_kernel, dim3((unsigned)std::min<long>(ceil_div(N * (d / 4), 256), 2048)),
-                           dim3(256), 0, st, dh_reduction(b, prev_ks));
+      if (need_dh && L.dhpart && (!fold || u + 1 == units)) {
+        // this unit's partials (the last band's go to the output: mode 0, 3 or 4)
+        long m0, rows;
+        block_span(r, m0, rows);
+        hipLaunchKernelGGL(dh_reduce_kernel, dim3((unsigned)std::min<long>(ceil_div(rows * (d / 4), 256), 2048)),
+                           dim3(256), 0, st, dh_reduction(u, prev_ks));
         HIP_TRY(hipGetLastError());
       }
       if (need_db) {
-        rc = colsum_band(b, G);
+        rc = colsum_unit(b, r, G);
         if (rc) return rc;
       }
     }
     return CCE_OK;
   }
 
-  // d not a multiple of 64: one G buffer; per band the recompute (register-
+  // d not a multiple of 64: one G buffer; per unit the recompute (register-
   // staged pipeline), then dH and dW
-  for (long b = 0; b < nbands; ++b) {
-    long v0, vb, vb64;
-    band_cols(b, v0, vb, vb64);
+  for (long u = 0; u < units; ++u) {
+    const long b = u / R, r = u % R;
     GemmShape g1 = {};
     GradParams e1 = {};
     int nb1 = 0;
-    grad_shape(H, W, bias, L, L.G[0], N, d, Vb, v0, vb, kSlowBN, false, g1, e1, nb1);
+    {
+      long v0, vb, vb64, m0, rows;
+      band_cols(b, v0, vb, vb64);
+      block_span(r, m0, rows);
+      grad_shape(H, W, bias, L, L.G[0], m0, rows, d, v0, vb, kSlowBN, false, g1, e1, nb1);
+    }
     rc = bias ? launch_gemm<kSlowBN, kWarp8, true, true, EpiGradBias, 3>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false)
               : launch_gemm<kSlowBN, kWarp8, true, true, EpiGrad, 3>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false);
     if (rc) return rc;
     GemmShape g2 = {}, g3 = {};
     AccParams e2 = {}, e3 = {};
     if (need_dh) {
-      rc = transpose_band(b);
-      if (rc) return rc;
-      dh_shape(b, L.G[0], 0, d, g2, e2);
+      if (r == 0) {
+        rc = transpose_band(b);
+        if (rc) return rc;
+      }
+      dh_shape(b, r, L.G[0], 0, d, g2, e2);
     }
-    if (need_dw) dw_shape(b, L.G[0], 0, d, g3, e3);
+    if (need_dw) dw_shape(b, r, L.G[0], 0, d, g3, e3);
     if (need_dh && need_dw)
       rc = launch_dual_acc(g3, e3, g2, e2, st);
     else if (need_dh)
@@ -2851,7 +2964,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       rc = launch_acc<kSlowBN, false, 5>(g3, e3, st, CCE_KERNEL_BWD_DW);
     if (rc) return rc;
     if (need_db) {
-      rc = colsum_band(b, L.G[0]);
+      rc = colsum_unit(b, r, L.G[0]);
       if (rc) return rc;
     }
   }

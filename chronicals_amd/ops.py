@@ -122,7 +122,7 @@ def cce_bwd(grad_out: Tensor, hidden: Tensor, weight: Tensor, labels: Tensor, ls
                          device=device)
         db = torch.empty((V,) if need_db else (0,), dtype=torch.float32, device=device)
         if need_dh or need_dw or need_db:
-            ws = torch.empty(_lib.backward_workspace_bytes(N, d, V, chunk_size, need_dh, need_dw),
+            ws = torch.empty(_lib.backward_workspace_bytes(N, d, V, chunk_size, need_dh, need_dw, dh_f32, dw_f32),
                              dtype=torch.uint8, device=device)
             _lib.check(lib.cce_backward(
                 g.data_ptr(), hidden.data_ptr(), weight.data_ptr(), labels.data_ptr(),

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define CCE_ABI_VERSION 5
+#define CCE_ABI_VERSION 6
 
 #define CCE_OK 0
 #define CCE_ERR_INVALID_ARG 1
@@ -129,9 +129,12 @@ int cce_forward_noalloc(const void* hidden, const void* weight, const void* labe
                         float label_smoothing, float z_loss_weight, int smoothing_form, int reduction, int lse_rows,
                         float* loss_out, float* lse_out, float* target_out, int32_t* n_valid_out, void* stream);
 
-/* Workspace bytes cce_backward needs (chunk_size = vocabulary band width). */
-int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_size,
-                                 int need_grad_hidden, int need_grad_weight, size_t* bytes);
+/* Workspace bytes cce_backward needs for this problem, chunk_size and these
+   gradients (grad_*_dtype: CCE_DTYPE_BF16 or CCE_DTYPE_F32, as passed to
+   cce_backward; fp32 gradients accumulate in place and need less). */
+int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_size, int need_grad_hidden,
+                                 int grad_hidden_dtype, int need_grad_weight, int grad_weight_dtype,
+                                 size_t* bytes);
 
 /*
  * Backward.  Replaces CutCrossEntropyBackward.backward
@@ -146,13 +149,17 @@ int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_
  * Any of grad_hidden / grad_weight / grad_bias may be NULL to skip it (a
  * frozen lm_head skips grad_weight, as triton_kernels.py:3213 does).
  * grad_*_dtype selects CCE_DTYPE_BF16 or CCE_DTYPE_F32 output; grad_bias is
- * fp32.  The vocabulary is processed in bands of chunk_size columns (rounded
- * up to a multiple of 256; the partial band, if any, first), the reference's
- * chunk_size argument (:1028); from 1024 to 4095 rows the bands are up to
- * 4x wider, while G and W^T of a band take no more than at 4096 rows and
- * chunk_size.  Deterministic: every reduction runs in a fixed
- * order, including the fp32 partials of dH when few rows make the library
- * split each band's columns over several workgroups.
+ * fp32.  The vocabulary is processed in bands of up to 8192 columns: the
+ * reference's chunk_size argument (:1028), rounded up to a multiple of 256,
+ * bounds the band from above (the partial band, if any, comes first); from
+ * 1024 to 4095 rows the bands are up to 4x wider, while G and W^T of a band
+ * take no more than at 4096 rows.  The rows are processed in blocks whose
+ * band gradient (two bf16 buffers of rows x band) stays within 512 MiB, so
+ * that memory does not grow with N; dW of a band accumulates over the
+ * blocks.  fp32 gradients accumulate in place; bf16 ones in fp32 workspace.
+ * Deterministic: every reduction runs in a fixed order, including the fp32
+ * partials of dH when few rows make the library split each band's columns
+ * over several workgroups.
  */
 int cce_backward(const float* grad_out, const void* hidden, const void* weight, const void* labels,
                  int labels_int64, const float* bias, const float* lse, const int32_t* n_valid,

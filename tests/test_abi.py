@@ -122,11 +122,36 @@ def test_workspace_queries(lib):
     assert _lib.forward_workspace_bytes(0, 64, 300, _lib.CCE_REDUCTION_MEAN) > 0
     assert _lib.forward_workspace_bytes(0, 64, 300, _lib.CCE_REDUCTION_NONE) > 0
     assert _lib.backward_workspace_bytes(0, 64, 300, 8192, True, True) >= 0
-    # chunk_size bounds the band; bands wider than 2^20 columns are clamped
+    # chunk_size bounds the band from above; the band is at most 8192 columns
+    # (the trainer's get_optimal_chunk_size gives 16384 at V >= 128K)
     assert _lib.backward_workspace_bytes(16384, 896, 151936, 2048, True, True) < b
+    assert _lib.backward_workspace_bytes(16384, 896, 151936, 16384, True, True) == b
     assert (_lib.backward_workspace_bytes(64, 64, 2 ** 22, 2 ** 22, True, True)
             == _lib.backward_workspace_bytes(64, 64, 2 ** 22, 2 ** 20, True, True))
     assert _lib.forward_workspace_bytes(2 ** 21, 64, 1000, _lib.CCE_REDUCTION_MEAN) > 0  # the largest N
+    # fp32 gradients accumulate in place: no fp32 dH / dW accumulators
+    assert _lib.backward_workspace_bytes(16384, 896, 151936, 8192, True, True, True, True) < b
+
+
+@pytest.mark.parametrize("d,V", [(896, 151936), (3584, 152064), (128, 50257)])
+def test_backward_band_gradient_bounded_in_N(lib, d, V):
+    """The band gradient G (two bf16 buffers of rows x band) is processed in
+    row blocks within a 512 MiB budget, so past one block the workspace grows
+    only by the O(N*d) buffers (H in row order, its transpose, the fp32 dH
+    accumulator: 8*d bytes per row) and the O(N) row data, never by N*band."""
+    per_row = 8 * d + 64
+    n1, n2 = 2 ** 17, 2 ** 21
+    w1 = _lib.backward_workspace_bytes(n1, d, V, 8192, True, True)
+    w2 = _lib.backward_workspace_bytes(n2, d, V, 8192, True, True)
+    assert w2 - w1 <= (n2 - n1) * per_row
+    # at the largest batch, all but the O(N*d) buffers fit in the G budget plus
+    # the band's W^T (two buffers) and fp32 dW accumulator
+    band_rest = 512 * 2 ** 20 + 2 * d * 8192 * 2 + 8192 * d * 4 + 2 ** 20
+    assert w2 - n2 * per_row <= band_rest
+    # a query for a gradient dtype other than bf16 / fp32 is refused
+    out = ctypes.c_size_t(0)
+    assert lib.cce_backward_workspace_bytes(1024, d, V, 8192, 1, 7, 1, 0, ctypes.byref(out)) == \
+        _lib.CCE_ERR_INVALID_ARG
 
 
 @pytest.mark.parametrize("N,d,V,red,msg", [

@@ -465,11 +465,15 @@ def test_peak_memory_below_materialised_logits(gpu):
     assert p_cce < 0.8 * p_mat, (p_cce, p_mat)
 
 
-def test_peak_memory_bounded_by_chunk_at_C2(gpu):
-    """At C2 the fwd+bwd holds O(N*chunk + N*d) extra memory, never the N x V logits."""
+@pytest.mark.parametrize("cfg", ["C2", "C5"])
+def test_peak_memory_bounded(gpu, cfg):
+    """The fwd+bwd holds the gradients, the backward workspace (O(N*d) buffers
+    plus a band gradient bounded by its 512 MiB budget: at C5 four row blocks)
+    and the forward's, never the N x V logits."""
     from chronicals_amd import _lib
     from chronicals_amd.kernels.cut_cross_entropy import cut_cross_entropy
-    N, d, V, chunk = 16384, 896, 151936, 8192
+    N, d, V = {"C2": (16384, 896, 151936), "C5": (65536, 3584, 152064)}[cfg]
+    chunk = 8192
     g = torch.Generator(device=gpu).manual_seed(0)
     h = torch.randn(N, d, generator=g, device=gpu).to(torch.bfloat16).requires_grad_(True)
     w = (torch.randn(V, d, generator=g, device=gpu) * 0.02).to(torch.bfloat16).requires_grad_(True)
@@ -484,10 +488,14 @@ def test_peak_memory_bounded_by_chunk_at_C2(gpu):
     bound = (grads + _lib.backward_workspace_bytes(N, d, V, chunk, True, True)
              + _lib.forward_workspace_bytes(N, d, V, _lib.CCE_REDUCTION_MEAN, _lib.CCE_LSE_LABELLED_ROWS)
              + 64 * 2 ** 20)
-    print(f"C2 peak extra {peak / 2**20:.0f} MiB, bound {bound / 2**20:.0f} MiB, "
+    print(f"{cfg} peak extra {peak / 2**20:.0f} MiB, bound {bound / 2**20:.0f} MiB, "
           f"materialised fp32 logits + grad {N * V * 8 / 2**20:.0f} MiB", flush=True)
     assert peak <= bound
     assert peak < 0.1 * N * V * 8
+    # what is not O(N*d) (H in row order, its transpose, the fp32 dH
+    # accumulator, the gradients) is the bounded band state
+    ws = _lib.backward_workspace_bytes(N, d, V, chunk, True, True)
+    assert ws - N * (8 * d + 64) <= 512 * 2 ** 20 + 2 * d * chunk * 2 + chunk * d * 4 + 2 ** 20
 
 
 @pytest.mark.parametrize("scale", [30.0, 300.0])
@@ -539,3 +547,40 @@ def test_linear_cross_entropy_name(gpu):
     got = {"loss": loss.detach().cpu().numpy(), "dh": hd.grad.float().cpu().numpy(),
            "dw": wd.grad.float().cpu().numpy(), "db": bd.grad.float().cpu().numpy()}
     compare(got, run_oracle(h, w, lab, b, reduction="sum"), "linear_cross_entropy")
+
+
+@pytest.mark.parametrize("N,d,V,chunk,budget_mb,hdtype,reduction,bias,frozen,ignore_frac", [
+    # 6 row blocks of 256 (2048-column bands); dH split 4 ways per block, folded into the next launch
+    (1300, 128, 9000, 1024, 2, torch.bfloat16, "mean", False, False, 0.1),
+    # fp32 gradients accumulate in place over bands (dH) and blocks (dW); dB added over the blocks
+    (2100, 256, 7000, 2048, 4, torch.float32, "sum", True, False, 0.1),
+    # d % 64 != 0: the unbanded path in 4 blocks, per-row grad_output
+    (1000, 72, 5000, 1024, 1, torch.bfloat16, "none", True, False, 0.1),
+    # frozen weight (dH only), 6 blocks of 512
+    (3000, 512, 12000, 4096, 8, torch.bfloat16, "mean", False, True, 0.1),
+    # 60% of the rows ignored: the blocks past the live rows have no rows to run; 256 + 128-wide dH tiles
+    (2600, 320, 8000, 2048, 4, torch.float32, "mean", False, False, 0.6),
+    # 3 blocks of 2048 rows x 16 hidden tiles: dH unsplit
+    (4500, 4096, 2000, 1024, 8, torch.bfloat16, "mean", True, False, 0.05),
+])
+def test_row_blocks(gpu, monkeypatch, N, d, V, chunk, budget_mb, hdtype, reduction, bias, frozen, ignore_frac):
+    """A backward whose band gradient exceeds the memory budget runs in row
+    blocks (CHRONICALS_CCE_G_BUDGET_MB shrinks the budget so small problems
+    take several): dW and dB of a band accumulate over the blocks, dH over the
+    bands; against the oracle and bitwise repeatable."""
+    from chronicals_amd import _lib
+    print(f"case row blocks N={N} d={d} V={V} chunk={chunk} budget={budget_mb}MiB {hdtype} {reduction}", flush=True)
+    f32 = hdtype == torch.float32
+    ws_default = _lib.backward_workspace_bytes(N, d, V, chunk, True, not frozen, f32, f32)
+    monkeypatch.setenv("CHRONICALS_CCE_G_BUDGET_MB", str(budget_mb))
+    # the budget took effect (the band gradient shrinks; an fp32 dW accumulator may be added)
+    assert _lib.backward_workspace_bytes(N, d, V, chunk, True, not frozen, f32, f32) != ws_default
+    h, w, lab, b = _rand_case(N, d, V, seed=N + d + 7, ignore_frac=ignore_frac, bias=bias)
+    go = torch.rand(N, generator=torch.Generator().manual_seed(5)) if reduction == "none" else None
+    kw = dict(chunk=chunk, reduction=reduction, grad_output=go, hdtype=hdtype, wdtype=hdtype, need_dw=not frozen)
+    got = run_hip(gpu, h, w, lab, b, **kw)
+    compare(got, run_oracle(h, w, lab, b, chunk=chunk, reduction=reduction, grad_output=go), f"blocks N{N}d{d}")
+    again = run_hip(gpu, h, w, lab, b, **kw)
+    assert np.array_equal(got["dh"], again["dh"])
+    if not frozen:
+        assert np.array_equal(got["dw"], again["dw"])
