@@ -435,10 +435,18 @@ struct LseParams {
   int tiles_n;
 };
 
-// Vocabulary splits per row tile of a forward whose rows were compacted:
-// all nb workgroups share the gl live row tiles, so the split count and the
-// partials' row stride (whole live tiles) follow the device-side live count.
-__device__ inline int lse_dyn_splits(int nb, int gl, int tiles_n) { return max(1, min(nb / gl, tiles_n)); }
+// Vocabulary splits per row tile of a forward whose rows were compacted: the
+// split count follows the device-side count of live row tiles, and
+// compact_rows_kernel stores it in live[1] (split_cost picks it).
+//
+// Cost of s splits over gl row tiles of tn vocabulary tiles on ncu CUs, in
+// tile-times: the gl*s equal workgroups run in ceil(gl*s / ncu) rounds of
+// ceil(tn / s) tiles each, plus about 0.15 tile of pipeline start per
+// workgroup.  The last round's idle CUs are what a good s avoids.
+__host__ __device__ inline float split_cost(int gl, int tn, int s, int ncu) {
+  const int rounds = (gl * s + ncu - 1) / ncu;
+  return (float)rounds * ((float)((tn + s - 1) / s) + 0.15f);
+}
 
 // Forward: per-row online (max, sum-exp) in base 2 over the workgroup's run of
 // vocabulary tiles; at the end one partial per (row, split) is written.
@@ -454,7 +462,7 @@ struct EpiLseT {
   static __device__ inline void assign(const GemmShape& g, const Params& p, int bid, int nb, int& tm,
                                        int& t0, int& t1, int& split) {
     const int gm = (g.M + kBM - 1) / kBM;
-    const int S = g.dyn == kDynM ? lse_dyn_splits(nb, gm, p.tiles_n) : p.splits;
+    const int S = g.dyn == kDynM ? g.live[1] : p.splits;
     if (bid >= gm * S) {  // a compacted forward uses gm * S of the nb workgroups
       t0 = t1 = 0;
       return;
@@ -1281,15 +1289,14 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(
   // wave w handles partial row i; its source row is idx[i] (identity without
   // idx).  With labelled_only, ignored rows get lse 0 and their partials,
   // which the compacted GEMM may not have written, are not read.  A
-  // compacted forward (live set) split the vocabulary into
-  // lse_dyn_splits(nb_fwd, live tiles, tiles_n) parts with whole live tiles
-  // as the partials' row stride.
+  // compacted forward (live set) split the vocabulary into live[1] parts with
+  // whole live tiles as the partials' row stride.
   const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int i = blockIdx.x * 4 + w;
   long ldp = N;
   if (live) {
     const int gl = (live[0] + kBM - 1) / kBM;
-    splits = lse_dyn_splits(nb_fwd, gl, tiles_n);
+    splits = live[1];
     ldp = (long)gl * kBM;
   }
   __shared__ float s_loss[4];
@@ -1767,7 +1774,8 @@ __global__ __launch_bounds__(kFusedThreads) void ce_logits_fused_kernel(
 // coefficients (backward) or are not read back (forward).
 __global__ __launch_bounds__(1024) void compact_rows_kernel(const void* labels, int labels64, int N,
                                                             long ignore_index, int* __restrict__ idx,
-                                                            int* __restrict__ live) {
+                                                            int* __restrict__ live, int nb_fwd, int tiles_n,
+                                                            int ncu) {
   // Rounds of 16384 rows; thread t owns the 16 consecutive rows t*16 ..
   // t*16+15 of a round, packs their valid bits into a mask, and one
   // block-wide exclusive scan of the per-thread counts places them.
@@ -1828,9 +1836,35 @@ __global__ __launch_bounds__(1024) void compact_rows_kernel(const void* labels, 
     }
     __syncthreads();
   }
-  if (tid == 0) {
-    const long tiles = base[0] > 0 ? (base[0] + kBM - 1) / kBM : 1;
-    live[0] = (int)(tiles * kBM < N ? tiles * kBM : N);
+  const int tiles = base[0] > 0 ? (base[0] + kBM - 1) / kBM : 1;
+  if (tid == 0) live[0] = (int)((long)tiles * kBM < N ? (long)tiles * kBM : N);
+  if (nb_fwd > 0) {
+    // the forward's vocabulary splits over the live row tiles (live[1]): the
+    // cheapest s of at most nb_fwd / tiles workgroups per row tile by
+    // split_cost, and at least enough for 4 rounds of workgroups when the
+    // launch allows (long single-round schedules leave CUs idle at the end);
+    // thread t prices s = t + 1, ties go to the larger s
+    const int gl = (int)((min((long)tiles * kBM, (long)N) + kBM - 1) / kBM);
+    const int smax = max(1, min(min(nb_fwd / gl, tiles_n), 1024));
+    const int smin = min(smax, max(1, (4 * ncu + gl - 1) / gl));
+    __shared__ float cost[1024];
+    __shared__ int arg[1024];
+    const int sv = tid + 1;
+    cost[tid] = (sv >= smin && sv <= smax) ? split_cost(gl, tiles_n, sv, ncu) : FLT_MAX;
+    arg[tid] = sv;
+    __syncthreads();
+    for (int o = 512; o >= 1; o >>= 1) {
+      if (tid < o) {
+        const float c2 = cost[tid + o];
+        const int a2 = arg[tid + o];
+        if (c2 < cost[tid] || (c2 == cost[tid] && a2 > arg[tid])) {
+          cost[tid] = c2;
+          arg[tid] = a2;
+        }
+      }
+      __syncthreads();
+    }
+    if (tid == 0) live[1] = arg[0];
   }
 }
 
@@ -2053,12 +2087,27 @@ int forward_splits(long N, long d, long V, bool compact) {
   const long gm = ceil_div(N, kBM), tn = ceil_div(V, lse_bn(d));
   // about 512 workgroups for few row tiles (runs of several vocabulary tiles,
   // so the pipeline's start is paid once per run), never fewer splits than
-  // min(32, 2048 / row tiles): large batches keep their split counts
+  // min(32, 2048 / row tiles): large batches keep their split counts.  A
+  // compacted forward launches room for 64 per row tile; its device-side
+  // choice (compact_rows_kernel) uses as many as split_cost favours.
   long s = std::max(ceil_div(512, gm), std::min<long>(32, ceil_div(2048, gm)));
-  if (compact && s < 32) s = 32;
+  if (compact && s < 64) s = 64;
   if (s > tn) s = tn;
   if (s < 1) s = 1;
   return (int)s;
+}
+
+// CUs of the current device (cached per device).
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
 }
 
 // Vocabulary band width: chunk rounded up to a multiple of 256, at most
@@ -2152,7 +2201,7 @@ FwdLayout fwd_layout(void* ws, long N, long d, long V, int reduction, int lse_ro
   L.wpart = c.take<float>((size_t)L.wsplits * d);
   L.wsum = c.take<float>((size_t)d + 1);
   L.idx = compact ? c.take<int>((size_t)N) : nullptr;
-  L.live = compact ? c.take<int>(1) : nullptr;
+  L.live = compact ? c.take<int>(2) : nullptr;  // live rows, vocabulary splits
   L.Hc = compact ? c.take<bf16_t>((size_t)N * d) : nullptr;
   L.bytes = align_up(c.off, 256);
   return L;
@@ -2468,7 +2517,7 @@ int forward_run(const void* hidden, const void* weight, const void* labels, int 
   // over the row tiles that hold them (the partials then follow that order)
   if (L.idx) {
     hipLaunchKernelGGL(compact_rows_kernel, dim3(1), dim3(1024), 0, st, labels, labels_int64, (int)N,
-                       (long)ignore_index, L.idx, L.live);
+                       (long)ignore_index, L.idx, L.live, gm * S, (int)ceil_div(V, lse_bn(d)), device_cus());
     HIP_TRY(hipGetLastError());
     const long chunks = (long)N * (d / 8);
     hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)std::min<long>(ceil_div(chunks, 256), 8192)), dim3(256), 0,
@@ -2682,7 +2731,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
   // GEMMs then skip the row tiles past them); the rest of dH is zeroed here.
   if (L.idx) {
     hipLaunchKernelGGL(compact_rows_kernel, dim3(1), dim3(1024), 0, st, labels, labels_int64, (int)N,
-                       (long)ignore_index, L.idx, L.live);
+                       (long)ignore_index, L.idx, L.live, 0, 0, 0);
     HIP_TRY(hipGetLastError());
     const long chunks = (long)N * (d / 8);
     hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)std::min<long>(ceil_div(chunks, 256), 8192)), dim3(256), 0,
