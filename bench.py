@@ -226,6 +226,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="C2")
     ap.add_argument("--chunk", type=int, default=8192)
+    ap.add_argument("--rows", type=int, default=None,
+                    help="run the configuration with this many rows (N) instead of its own (smaller batches at "
+                         "the configuration's d and V)")
     ap.add_argument("--cpu-rows", type=int, default=None,
                     help="rows of the CPU baseline sample (default 4096 fused, 8192 logits)")
     ap.add_argument("--skip-cpu", action="store_true")
@@ -269,6 +272,9 @@ def main() -> int:
     from tests.cce_common import CONFIGS, make_inputs
 
     cfg = CONFIGS[args.config]
+    if args.rows:
+        import dataclasses
+        cfg = dataclasses.replace(cfg, N=int(args.rows))
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     h, w, lab = make_inputs(cfg, seed=0, device=dev, gen_device="cuda")
@@ -344,7 +350,7 @@ def main() -> int:
         with open(TRAFFIC_FILE) as f:
             tr = json.load(f)
         if (tr.get("config") == cfg.name and tr.get("kernel") == dom and not args.frozen_weight
-                and not args.trainer and chunk == tr.get("chunk_size", 8192)):
+                and not args.trainer and not args.rows and chunk == tr.get("chunk_size", 8192)):
             traffic = tr.get("hbm_bytes_per_launch")
             clock = tr.get("mfma_busy_and_clock", {}).get(dom, {}).get("clock_ghz")
     except (OSError, ValueError):

@@ -115,7 +115,8 @@ class CCEError(RuntimeError):
 
 
 def lib_path() -> str:
-    return os.environ.get("CHRONICALS_CCE_LIB", _build.LIB_PATH)
+    """The library to load: CHRONICALS_CCE_LIB when set and non-empty, else the in-tree build."""
+    return os.environ.get("CHRONICALS_CCE_LIB") or _build.LIB_PATH
 
 
 def load() -> ctypes.CDLL:
