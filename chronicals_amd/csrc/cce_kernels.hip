@@ -234,6 +234,11 @@ struct GemmShape {
   // The DMA's buffer range still ends where B's rows end, so a slab that runs
   // past K reads the next row's (finite) values or zeros, never memory past B.
   int kb = 0;
+  // Row map of a K-major A (PIPE 4): GEMM row m is row arow[m] of A, which
+  // has arows rows in all (arows * lda * 2 bytes below 2^31 - 16).  Null:
+  // row m is row m.
+  const int* arow = nullptr;
+  long arows = 0;
 };
 
 // Live rows of a row block that starts at row `base` of the compacted order.
@@ -317,6 +322,41 @@ __device__ inline void dma_kmajor(const bf16_t* __restrict__ X, long ld, int r0,
         rs, (__attribute__((address_space(3))) void*)(S + blk * 512), 16, voff, k0 * 2, 0, 0);
   }
 }
+
+// The K-major A tile a workgroup streams (rows [r0, r0 + kBM) of a GEMM with
+// rlim rows) read through a row map: GEMM row m is row arow[m] of A, which
+// has arows rows.  The buffer descriptor spans all of A; for each DMA
+// instruction j of the wave, each lane keeps the byte offset of its 16-byte
+// chunk at k = 0 (the slab's k0 goes in the instruction's scalar offset),
+// computed once per workgroup.  Rows past rlim get an offset past the descriptor's
+// range and read as zero.
+template <int W>
+struct ARows {
+  static constexpr int kI = kBM / (8 * W);
+  const bf16_t* base;
+  long bytes;
+  int voff[kI];
+  __device__ inline void init(const bf16_t* __restrict__ X, long ld, int r0, int rlim, const int* __restrict__ arow,
+                              long arows, int w, int l) {
+    const long rows_left = (long)rlim - r0;
+    base = X;
+    bytes = arows * ld * 2;
+#pragma unroll
+    for (int j = 0; j < kI; ++j) {
+      const int row = (w * kI + j) * 8 + (l >> 3);
+      const int c = (l & 7) ^ swz(row);
+      voff[j] = row < rows_left ? (int)(((long)arow[r0 + row] * ld + c * 8) * 2) : (int)0x80000000u;
+    }
+  }
+  // the DMA of k [k0, k0 + 64) into the swizzled LDS region S
+  __device__ inline void dma(int k0, bf16_t* S, int w) const {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, bytes);
+#pragma unroll
+    for (int j = 0; j < kI; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (__attribute__((address_space(3))) void*)(S + (w * kI + j) * 512), 16, voff[j], k0 * 2, 0, 0);
+  }
+};
 
 // MN-major tile for PIPE 5: element (m, k) at X[k*ld + m].  The tile
 // k [k0, k0 + 64) x m [m0, m0 + 256) is copied in its natural [k][m] layout
@@ -858,7 +898,8 @@ constexpr int gemm_lds_elems(int pipe, int nst = 2) {
   return (pipe >= 4 ? nst : 2) * (kBM + BN) * (pipe >= 4 ? 64 : kPitch);
 }
 
-template <int BN, int W, bool AK, bool BKM, template <int, int> class EpiT, int PIPE, int NST = 2>
+// AROW: A is read through g.arow (PIPE 4; see ARows).
+template <int BN, int W, bool AK, bool BKM, template <int, int> class EpiT, int PIPE, int NST = 2, bool AROW = false>
 __device__ __forceinline__ void gemm_body(const GemmShape& g_in, const typename EpiT<BN, W>::Params& ep, int bid,
                                           int nb, bf16_t* smem) {
   static_assert(PIPE >= 3 && PIPE <= 5, "pipelines: 3 (register-staged), 4 and 5 (direct-to-LDS)");
@@ -927,8 +968,14 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g_in, const typename 
     };
     // DMA of the next unissued slab (tile it2, k-slab ik2) into stage S
     int it2 = t0, ik2 = 0;
+    // A through a row map: its lane offsets are computed once per workgroup
+    static_assert(!AROW || PIPE == 4, "row-mapped A is K-major");
+    ARows<W> arows;
+    if constexpr (AROW) arows.init(g.A, g.lda, a_r0, g.M, g.arow, g.arows, w, l);
     auto issue = [&](bf16_t* S) {
-      if constexpr (PIPE == 4)
+      if constexpr (AROW)
+        arows.dma(ik2 * kBK, S, w);
+      else if constexpr (PIPE == 4)
         dma_kmajor<kBM, W>(g.A, g.lda, a_r0, g.M, ik2 * kBK, S, w, l);
       else
         dma_mnmajor256<W>(g.A, g.lda, a_r0, ik2 * kBK, g.K, S, w, l);
@@ -1086,10 +1133,10 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g_in, const typename 
   Epi::finish(ep, st, g, tm, split, smem, wm, wn, l);
 }
 
-template <int BN, int W, bool AK, bool BKM, template <int, int> class EpiT, int PIPE, int NST = 2>
+template <int BN, int W, bool AK, bool BKM, template <int, int> class EpiT, int PIPE, int NST = 2, bool AROW = false>
 __global__ __launch_bounds__(W * 64) void gemm_kernel(GemmShape g, typename EpiT<BN, W>::Params ep) {
   __shared__ __attribute__((aligned(16))) bf16_t smem[gemm_lds_elems<BN>(PIPE, NST) + EpiT<BN, W>::kScratch];
-  gemm_body<BN, W, AK, BKM, EpiT, PIPE, NST>(g, ep, blockIdx.x, gridDim.x, smem);
+  gemm_body<BN, W, AK, BKM, EpiT, PIPE, NST, AROW>(g, ep, blockIdx.x, gridDim.x, smem);
 }
 
 // dW and dH GEMMs of one vocabulary band in a single launch.  The first
@@ -1220,9 +1267,11 @@ __device__ inline void dh_split_body(const GemmShape& g0, const AccParams& e0, i
 
 template <int NT>
 __device__ inline void transpose_tile(const bf16_t* __restrict__ in, long ldi, int R, int C, bf16_t* __restrict__ out,
-                                      long ldo, int Rpad, int r0, int c0, bf16_t (*t)[66], int tid);
+                                      long ldo, int Rpad, int r0, int c0, bf16_t (*t)[66], int tid,
+                                      const int* __restrict__ rmap);
 
-template <bool HB>
+// AROW: the recompute reads H's rows through the row order.
+template <bool HB, bool AROW>
 __global__ __launch_bounds__(kWarp8 * 64) void band_kernel(BandLaunch p) {
   __shared__ __attribute__((aligned(16))) bf16_t smem[gemm_lds_elems<kFastBN>(4) + EpiGrad<kFastBN, kWarp8>::kScratch];
   int b = blockIdx.x;
@@ -1254,9 +1303,9 @@ __global__ __launch_bounds__(kWarp8 * 64) void band_kernel(BandLaunch p) {
   b -= p.nb_dh2;
   if (b < p.nb_gr) {
     if constexpr (HB)
-      gemm_body<kFastBN, kWarp8, true, true, EpiGradBias, 4>(p.gr, p.e_gr, b, p.nb_gr, smem);
+      gemm_body<kFastBN, kWarp8, true, true, EpiGradBias, 4, 2, AROW>(p.gr, p.e_gr, b, p.nb_gr, smem);
     else
-      gemm_body<kFastBN, kWarp8, true, true, EpiGrad, 4>(p.gr, p.e_gr, b, p.nb_gr, smem);
+      gemm_body<kFastBN, kWarp8, true, true, EpiGrad, 4, 2, AROW>(p.gr, p.e_gr, b, p.nb_gr, smem);
     return;
   }
   b -= p.nb_gr;
@@ -1266,7 +1315,7 @@ __global__ __launch_bounds__(kWarp8 * 64) void band_kernel(BandLaunch p) {
   }
   b -= p.nb_red;
   transpose_tile<kWarp8 * 64>(p.tr.in, p.tr.ldi, p.tr.R, p.tr.C, p.tr.out, p.tr.ldo, p.tr.Rpad, (b % p.tr.tiles_r) * 64,
-                              (b / p.tr.tiles_r) * 64, reinterpret_cast<bf16_t(*)[66]>(smem), threadIdx.x);
+                              (b / p.tr.tiles_r) * 64, reinterpret_cast<bf16_t(*)[66]>(smem), threadIdx.x, nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -1932,16 +1981,21 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__
 }
 
 // out[c][r] = in[r][c] for r < R (zero for R <= r < Rpad), c < C, over the
-// 64 x 64 tile at (r0, c0), by NT threads staging through t.
+// 64 x 64 tile at (r0, c0), by NT threads staging through t.  With a row map,
+// row r of the input is row rmap[r] of in.
 template <int NT>
 __device__ inline void transpose_tile(const bf16_t* __restrict__ in, long ldi, int R, int C, bf16_t* __restrict__ out,
-                                      long ldo, int Rpad, int r0, int c0, bf16_t (*t)[66], int tid) {
+                                      long ldo, int Rpad, int r0, int c0, bf16_t (*t)[66], int tid,
+                                      const int* __restrict__ rmap) {
 #pragma unroll
   for (int it = 0; it < 512 / NT; ++it) {
     const int q = tid + it * NT;         // 512 chunks of 8 elements
     const int rr = q >> 3, cc = (q & 7) * 8;
     u32x4 v = u32x4{0u, 0u, 0u, 0u};
-    if (r0 + rr < R && c0 + cc < C) v = *reinterpret_cast<const u32x4*>(in + (long)(r0 + rr) * ldi + c0 + cc);
+    if (r0 + rr < R && c0 + cc < C) {
+      const long r = rmap ? (long)rmap[r0 + rr] : (long)(r0 + rr);
+      v = *reinterpret_cast<const u32x4*>(in + r * ldi + c0 + cc);
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       t[rr][cc + 2 * e] = (bf16_t)(v[e] & 0xffffu);
@@ -1963,9 +2017,10 @@ __device__ inline void transpose_tile(const bf16_t* __restrict__ in, long ldi, i
 }
 
 __global__ __launch_bounds__(256) void transpose_kernel(const bf16_t* __restrict__ in, long ldi, int R, int C,
-                                                        bf16_t* __restrict__ out, long ldo, int Rpad) {
+                                                        bf16_t* __restrict__ out, long ldo, int Rpad,
+                                                        const int* __restrict__ rmap) {
   __shared__ bf16_t t[64][66];
-  transpose_tile<256>(in, ldi, R, C, out, ldo, Rpad, blockIdx.x * 64, blockIdx.y * 64, t, threadIdx.x);
+  transpose_tile<256>(in, ldi, R, C, out, ldo, Rpad, blockIdx.x * 64, blockIdx.y * 64, t, threadIdx.x, rmap);
 }
 
 // dB[c] = sum_m G[m][c] for c < C (fixed order: deterministic).  Block = 64
@@ -2157,13 +2212,33 @@ long block_rows(long N, long Vb) {
   return nb >= n ? n : nb;
 }
 
+// The compacted GEMMs take H's rows either from a gathered copy (Hc, N x d
+// bf16 of workspace, written by gather_rows_kernel) or straight from H
+// through the row order (ARows).  Reading through the order costs each
+// workgroup a dependent load before its first slab (about 1.5% of a C2 band
+// launch, whose recompute workgroups run one tile each), so the copy is kept
+// while it is small next to the band state (H below 256 MiB); from there up
+// to the DMA's 32-bit lane offsets (2 GiB) the rows are read in place, and
+// past that the copy returns.  CHRONICALS_CCE_ROW_GATHER=0 forces the copy,
+// =1 reads in place wherever the offsets allow (read on every call, so a
+// workspace query and the call it sizes must see the same value).
+constexpr long kInPlaceMinBytes = 256L << 20;
+bool rows_in_place(long N, long d) {
+  const long bytes = N * d * 2;
+  if (bytes > 0x7ffffff0L) return false;
+  const char* e = getenv("CHRONICALS_CCE_ROW_GATHER");
+  if (e && (e[0] == '0' || e[0] == '1') && e[1] == 0) return e[0] == '1';
+  return bytes >= kInPlaceMinBytes;
+}
+
 struct FwdLayout {
   float *pm, *ps, *bsum, *rowloss;
   int* bcnt;
   float *wpart, *wsum;  // column sums of W by row split, and their total (+ the bias sum)
   int wsplits;
   // row compaction (CCE_LSE_LABELLED_ROWS, d a multiple of 64): row order,
-  // live row count, H in that order
+  // live row count, and H in that order when the GEMM cannot read H through
+  // the row order
   int* idx;
   int* live;
   bf16_t* Hc;
@@ -2202,12 +2277,13 @@ FwdLayout fwd_layout(void* ws, long N, long d, long V, int reduction, int lse_ro
   L.wsum = c.take<float>((size_t)d + 1);
   L.idx = compact ? c.take<int>((size_t)N) : nullptr;
   L.live = compact ? c.take<int>(2) : nullptr;  // live rows, vocabulary splits
-  L.Hc = compact ? c.take<bf16_t>((size_t)N * d) : nullptr;
+  L.Hc = compact && !rows_in_place(N, d) ? c.take<bf16_t>((size_t)N * d) : nullptr;
   L.bytes = align_up(c.off, 256);
   return L;
 }
 
 struct BwdLayout {
+  long N;        // rows
   long Vb, Nb;    // band width, rows per block
   int nblocks;    // row blocks
   float4* rowp;
@@ -2217,7 +2293,8 @@ struct BwdLayout {
   bf16_t* HT;
   float* dHacc;   // dH over the bands (bf16 dH with several bands; fp32 dH accumulates in place)
   float* dWacc;   // dW of a band over the row blocks (bf16 dW with several blocks)
-  // row compaction (banded backward): row order, live row count, H in that order
+  // row compaction (banded backward): row order, live row count, and H in
+  // that order when the GEMMs cannot read H through the row order
   int* idx;
   int* live;
   bf16_t* Hc;
@@ -2261,6 +2338,7 @@ BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bo
                      bool dw_f32) {
   Carver c(ws);
   BwdLayout L;
+  L.N = N;
   L.Vb = Vb;
   L.Nb = block_rows(N, Vb);
   L.nblocks = (int)ceil_div(std::max<long>(N, 1), L.Nb);
@@ -2279,7 +2357,7 @@ BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bo
   const bool compact = banded(d);
   L.idx = compact ? c.take<int>((size_t)N) : nullptr;
   L.live = compact ? c.take<int>(1) : nullptr;
-  L.Hc = compact ? c.take<bf16_t>((size_t)N * d) : nullptr;
+  L.Hc = compact && !rows_in_place(N, d) ? c.take<bf16_t>((size_t)N * d) : nullptr;
   L.dh_ks = need_dh ? dh_splits(L.Nb, d, Vb) : 1;
   // a second partial buffer only when the reduction rides in the next
   // launch (dh_fold); otherwise each unit's reduction runs before the next
@@ -2349,13 +2427,14 @@ double gemm_flops(long M, long N, long K) { return 2.0 * (double)M * (double)N *
 
 // A GEMM launch; `credited` is the algorithmic share of its FLOPs (the
 // logits recompute of the backward is executed but not credited).
-template <int BN, int W, bool AK, bool BK, template <int, int> class EpiT, int PIPE = 3, int NST = 2>
+template <int BN, int W, bool AK, bool BK, template <int, int> class EpiT, int PIPE = 3, int NST = 2,
+          bool AROW = false>
 int launch_gemm(const GemmShape& g, const typename EpiT<BN, W>::Params& ep, int nblocks, hipStream_t st,
                 int kind, bool credited) {
   if (nblocks <= 0) return CCE_OK;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   const bool timed = timing_begin(st, &e0, &e1);
-  hipLaunchKernelGGL((gemm_kernel<BN, W, AK, BK, EpiT, PIPE, NST>), dim3(nblocks), dim3(W * 64), 0, st, g, ep);
+  hipLaunchKernelGGL((gemm_kernel<BN, W, AK, BK, EpiT, PIPE, NST, AROW>), dim3(nblocks), dim3(W * 64), 0, st, g, ep);
   HIP_TRY(hipGetLastError());
   if (timed) {
     const double f = gemm_flops(g.M, g.N, g.K);
@@ -2412,7 +2491,14 @@ int launch_acc(const GemmShape& g, const AccParams& ep, hipStream_t st, int kind
 void grad_shape(const bf16_t* H, const bf16_t* W, const float* bias, const BwdLayout& L, bf16_t* G, long m0,
                 long rows, long d, long v0, long vb, int bn, bool in_band, GemmShape& g, GradParams& e, int& nb) {
   const int gm = (int)ceil_div(rows, kBM);
-  g.A = (L.Hc ? L.Hc : H) + m0 * d; g.lda = d; g.B = W + v0 * d; g.ldb = d;
+  if (L.Hc || !L.idx) {
+    g.A = (L.Hc ? L.Hc : H) + m0 * d;
+  } else {
+    g.A = H;
+    g.arow = L.idx + m0;
+    g.arows = L.N;
+  }
+  g.lda = d; g.B = W + v0 * d; g.ldb = d;
   g.M = (int)rows; g.N = (int)vb; g.K = (int)d;
   g.live = L.live; g.dyn = L.live ? kDynM : kDynNone; g.live_base = (int)m0;
   e.bias = bias; e.rowp = L.rowp + m0; e.rowlab = L.rowlab + m0; e.G = G; e.ldg = L.Vb; e.v0 = (int)v0;
@@ -2421,15 +2507,20 @@ void grad_shape(const bf16_t* H, const bf16_t* W, const float* bias, const BwdLa
   nb = gm * e.splits;
 }
 
-int launch_band(const BandLaunch& p, bool has_bias, hipStream_t st) {
+int launch_band(const BandLaunch& p, bool has_bias, hipStream_t st, int kind = CCE_KERNEL_BWD_BAND) {
   const int nb = p.nb_dw + p.nb_dw2 + p.nb_dh + p.nb_dh2 + p.nb_gr + p.nb_red + p.nb_tr;
   if (nb <= 0) return CCE_OK;
   hipEvent_t t0 = nullptr, t1 = nullptr;
   const bool timed = timing_begin(st, &t0, &t1);
-  if (has_bias)
-    hipLaunchKernelGGL(band_kernel<true>, dim3(nb), dim3(kWarp8 * 64), 0, st, p);
+  const bool arow = p.gr.arow != nullptr;
+  if (has_bias && arow)
+    hipLaunchKernelGGL((band_kernel<true, true>), dim3(nb), dim3(kWarp8 * 64), 0, st, p);
+  else if (has_bias)
+    hipLaunchKernelGGL((band_kernel<true, false>), dim3(nb), dim3(kWarp8 * 64), 0, st, p);
+  else if (arow)
+    hipLaunchKernelGGL((band_kernel<false, true>), dim3(nb), dim3(kWarp8 * 64), 0, st, p);
   else
-    hipLaunchKernelGGL(band_kernel<false>, dim3(nb), dim3(kWarp8 * 64), 0, st, p);
+    hipLaunchKernelGGL((band_kernel<false, false>), dim3(nb), dim3(kWarp8 * 64), 0, st, p);
   HIP_TRY(hipGetLastError());
   if (timed) {
     double cr = 0.0;
@@ -2438,7 +2529,7 @@ int launch_band(const BandLaunch& p, bool has_bias, hipStream_t st) {
     if (p.nb_dh) cr += gemm_flops(p.dh.M, p.dh.N, p.dh.K);
     if (p.nb_dh2) cr += gemm_flops(p.dh2.M, p.dh2.N, p.dh2.K);
     const double ex = cr + (p.nb_gr ? gemm_flops(p.gr.M, p.gr.N, p.gr.K) : 0.0);
-    timing_end(CCE_KERNEL_BWD_BAND, st, t0, t1, cr, ex);
+    timing_end(kind, st, t0, t1, cr, ex);
   }
   return CCE_OK;
 }
@@ -2519,14 +2610,20 @@ int forward_run(const void* hidden, const void* weight, const void* labels, int 
     hipLaunchKernelGGL(compact_rows_kernel, dim3(1), dim3(1024), 0, st, labels, labels_int64, (int)N,
                        (long)ignore_index, L.idx, L.live, gm * S, (int)ceil_div(V, lse_bn(d)), device_cus());
     HIP_TRY(hipGetLastError());
-    const long chunks = (long)N * (d / 8);
-    hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)std::min<long>(ceil_div(chunks, 256), 8192)), dim3(256), 0,
-                       st, static_cast<const bf16_t*>(hidden), (int)d, L.idx, (int)N, L.Hc);
-    HIP_TRY(hipGetLastError());
+    if (L.Hc) {
+      const long chunks = (long)N * (d / 8);
+      hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)std::min<long>(ceil_div(chunks, 256), 8192)), dim3(256),
+                         0, st, static_cast<const bf16_t*>(hidden), (int)d, L.idx, (int)N, L.Hc);
+      HIP_TRY(hipGetLastError());
+    }
   }
 
   GemmShape g;
   g.A = L.Hc ? L.Hc : static_cast<const bf16_t*>(hidden);
+  if (L.idx && !L.Hc) {
+    g.arow = L.idx;
+    g.arows = N;
+  }
   g.lda = d;
   g.B = static_cast<const bf16_t*>(weight);
   g.ldb = d;
@@ -2542,7 +2639,12 @@ int forward_run(const void* hidden, const void* weight, const void* labels, int 
   ep.ldp = N;
   ep.splits = S;
   ep.tiles_n = (int)ceil_div(V, lse_bn(d));
-  if (fast_k(d))
+  if (fast_k(d) && g.arow)
+    rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiLseBias, 4, 2, true>(g, ep, gm * S, st,
+                                                                                CCE_KERNEL_FWD_LSE, true)
+              : launch_gemm<kFastBN, kWarp8, true, true, EpiLse, 4, 2, true>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE,
+                                                                            true);
+  else if (fast_k(d))
     rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiLseBias, 4>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE, true)
               : launch_gemm<kFastBN, kWarp8, true, true, EpiLse, 4>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE, true);
   else
@@ -2733,10 +2835,12 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     hipLaunchKernelGGL(compact_rows_kernel, dim3(1), dim3(1024), 0, st, labels, labels_int64, (int)N,
                        (long)ignore_index, L.idx, L.live, 0, 0, 0);
     HIP_TRY(hipGetLastError());
-    const long chunks = (long)N * (d / 8);
-    hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)std::min<long>(ceil_div(chunks, 256), 8192)), dim3(256), 0,
-                       st, H, (int)d, L.idx, (int)N, L.Hc);
-    HIP_TRY(hipGetLastError());
+    if (L.Hc) {
+      const long chunks = (long)N * (d / 8);
+      hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)std::min<long>(ceil_div(chunks, 256), 8192)), dim3(256),
+                         0, st, H, (int)d, L.idx, (int)N, L.Hc);
+      HIP_TRY(hipGetLastError());
+    }
     if (need_dh) {
       const long row_bytes = d * (dh_f32 ? 4 : 2);
       hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)std::min<long>(ceil_div(N * (row_bytes / 16), 256), 4096)),
@@ -2750,7 +2854,8 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
   HIP_TRY(hipGetLastError());
   if (need_dw) {
     hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)ceil_div(N8, 64), (unsigned)ceil_div(d, 64)), dim3(256), 0,
-                       st, L.Hc ? L.Hc : H, (long)d, (int)N, (int)d, L.HT, (long)N8, (int)N8);
+                       st, L.Hc ? L.Hc : H, (long)d, (int)N, (int)d, L.HT, (long)N8, (int)N8,
+                       L.Hc ? nullptr : L.idx);
     HIP_TRY(hipGetLastError());
   }
 
@@ -2840,7 +2945,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     TransposeParams t;
     const int tiles = transpose_params(b, t);
     hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)t.tiles_r, (unsigned)(tiles / t.tiles_r)), dim3(256), 0, st,
-                       t.in, t.ldi, t.R, t.C, t.out, t.ldo, t.Rpad);
+                       t.in, t.ldi, t.R, t.C, t.out, t.ldo, t.Rpad, nullptr);
     HIP_TRY(hipGetLastError());
     return CCE_OK;
   };
@@ -2870,8 +2975,18 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       GradParams e1 = {};
       int nb1 = 0;
       grad_unit(0, false, kFastBN, g1, e1, nb1);
-      rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiGradBias, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false)
-                : launch_gemm<kFastBN, kWarp8, true, true, EpiGrad, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false);
+      if (g1.arow) {
+        // reading through the row order: the band kernel's code (with only
+        // this recompute population) keeps it within the registers
+        BandLaunch p0 = {};
+        p0.gr = g1;
+        p0.e_gr = e1;
+        p0.nb_gr = nb1;
+        rc = launch_band(p0, bias != nullptr, st, CCE_KERNEL_BWD_GRAD);
+      } else
+        rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiGradBias, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD,
+                                                                              false)
+                  : launch_gemm<kFastBN, kWarp8, true, true, EpiGrad, 4>(g1, e1, nb1, st, CCE_KERNEL_BWD_GRAD, false);
       if (rc) return rc;
       if (need_dh) {
         rc = transpose_band(0);

@@ -137,21 +137,52 @@ def test_workspace_queries(lib):
 def test_backward_band_gradient_bounded_in_N(lib, d, V):
     """The band gradient G (two bf16 buffers of rows x band) is processed in
     row blocks within a 512 MiB budget, so past one block the workspace grows
-    only by the O(N*d) buffers (H in row order, its transpose, the fp32 dH
-    accumulator: 8*d bytes per row) and the O(N) row data, never by N*band."""
+    only by the O(N*d) buffers (H's transpose, the fp32 dH accumulator and,
+    past 2 GiB of H, H in row order: at most 8*d bytes per row) and the O(N)
+    row data, never by N*band."""
     per_row = 8 * d + 64
     n1, n2 = 2 ** 17, 2 ** 21
     w1 = _lib.backward_workspace_bytes(n1, d, V, 8192, True, True)
     w2 = _lib.backward_workspace_bytes(n2, d, V, 8192, True, True)
-    assert w2 - w1 <= (n2 - n1) * per_row
-    # at the largest batch, all but the O(N*d) buffers fit in the G budget plus
-    # the band's W^T (two buffers) and fp32 dW accumulator
-    band_rest = 512 * 2 ** 20 + 2 * d * 8192 * 2 + 8192 * d * 4 + 2 ** 20
+    # at both batches, all but the O(N*d) buffers fit in the G budget plus
+    # the band's W^T (two buffers), its fp32 dW accumulator and the fp32
+    # partials of a K-split dH (about 128 tiles of 256 x 256, two buffers)
+    band_rest = 512 * 2 ** 20 + 2 * d * 8192 * 2 + 8192 * d * 4 + 2 * 160 * 256 * 256 * 4 + 2 ** 20
+    assert w1 - n1 * per_row <= band_rest
     assert w2 - n2 * per_row <= band_rest
+    assert w2 - w1 >= (n2 - n1) * 6 * d  # the O(N*d) buffers are there
     # a query for a gradient dtype other than bf16 / fp32 is refused
     out = ctypes.c_size_t(0)
     assert lib.cce_backward_workspace_bytes(1024, d, V, 8192, 1, 7, 1, 0, ctypes.byref(out)) == \
         _lib.CCE_ERR_INVALID_ARG
+
+
+def test_row_order_copy_policy(lib, monkeypatch):
+    """The compacted GEMMs read H through the row order when H takes 256 MiB
+    to 2 GiB (the byte offsets fit 32 bits and a gathered copy would be
+    large); below that, above it, or with CHRONICALS_CCE_ROW_GATHER=0 both
+    workspaces hold a gathered N x d bf16 copy of H.  =1 reads in place
+    wherever the offsets fit."""
+    def both(N, d):
+        return (_lib.backward_workspace_bytes(N, d, 152064, 8192, True, True),
+                _lib.forward_workspace_bytes(N, d, 152064, _lib.CCE_REDUCTION_MEAN, _lib.CCE_LSE_LABELLED_ROWS))
+    cases = {"C2": (16384, 896), "C5": (65536, 3584), "large": (2 ** 21, 1024)}   # H: 28 MiB, 448 MiB, 4 GiB
+    ws = {}
+    for env in (None, "0", "1"):
+        if env is None:
+            monkeypatch.delenv("CHRONICALS_CCE_ROW_GATHER", raising=False)
+        else:
+            monkeypatch.setenv("CHRONICALS_CCE_ROW_GATHER", env)
+        for k, nd in cases.items():
+            ws[k, env] = both(*nd)
+    def copy(k):
+        return cases[k][0] * cases[k][1] * 2
+    for i in range(2):
+        assert ws["C5", "0"][i] - ws["C5", None][i] == copy("C5")   # C5: in place by default
+        assert ws["C5", "1"][i] == ws["C5", None][i]
+        assert ws["C2", None][i] - ws["C2", "1"][i] == copy("C2")   # C2: the copy by default
+        assert ws["C2", "0"][i] == ws["C2", None][i]
+        assert ws["large", "1"][i] == ws["large", "0"][i] == ws["large", None][i]   # past 2 GiB: always the copy
 
 
 @pytest.mark.parametrize("N,d,V,red,msg", [
@@ -179,14 +210,14 @@ def test_lse_rows_option(lib):
     rc = lib.cce_forward(fake, fake, fake, 1, None, 64, 64, 1000, -100, 0.0, 0.0, _lib.CCE_SMOOTH_LOGV,
                          _lib.CCE_REDUCTION_MEAN, 7, fake, fake, None, fake, fake, 1 << 30, None)
     assert rc == _lib.CCE_ERR_INVALID_ARG and "lse_rows" in lib.cce_last_error().decode()
-    # labelled rows only: with d a multiple of 64 the forward reorders the rows (row order and a copy of
-    # the hidden rows in the workspace); with any other d it needs nothing more
+    # labelled rows only: with d a multiple of 64 the forward reorders the rows (the row order in the
+    # workspace; the GEMM reads H through it); with any other d it needs nothing more
     sizes = {}
     for d in (64, 72):
         for rows in (_lib.CCE_LSE_ALL_ROWS, _lib.CCE_LSE_LABELLED_ROWS):
             assert lib.cce_forward_workspace_bytes(300, d, 1000, 1, rows, ctypes.byref(out)) == _lib.CCE_OK
             sizes[d, rows] = out.value
-    assert sizes[64, 1] >= sizes[64, 0] + 300 * 64 * 2 + 300 * 4
+    assert sizes[64, 1] >= sizes[64, 0] + 300 * 4
     assert sizes[72, 1] == sizes[72, 0]
 
 

@@ -549,6 +549,36 @@ def test_linear_cross_entropy_name(gpu):
     compare(got, run_oracle(h, w, lab, b, reduction="sum"), "linear_cross_entropy")
 
 
+@pytest.mark.parametrize("N,d,V,chunk,budget_mb,ignore_frac,bias", [
+    (1500, 256, 5000, 2048, 0, 0.3, False),   # one block, 6 live row tiles of 6
+    (2100, 320, 7000, 1024, 2, 0.1, True),    # row blocks of 512 + bias; 256 + 128-wide dH tiles
+    (700, 128, 3000, 1024, 0, 0.97, False),   # 21 labelled rows: one live tile, the rest zero-filled
+])
+def test_row_order_reads_match_gathered_copy(gpu, monkeypatch, N, d, V, chunk, budget_mb, ignore_frac, bias):
+    """With CHRONICALS_CCE_ROW_GATHER=1 the compacted GEMMs read H's rows
+    through the row order (the default for H of 256 MiB to 2 GiB); with =0
+    they read a gathered copy of H (the default below and above).  Same
+    values in the same order: loss, dH, dW and dB bitwise equal, and the
+    copy's N x d bf16 shows in both workspaces."""
+    from chronicals_amd import _lib
+    print(f"case row order N={N} d={d} V={V} chunk={chunk} budget={budget_mb} ignore={ignore_frac}", flush=True)
+    if budget_mb:
+        monkeypatch.setenv("CHRONICALS_CCE_G_BUDGET_MB", str(budget_mb))
+    monkeypatch.setenv("CHRONICALS_CCE_ROW_GATHER", "1")
+    h, w, lab, b = _rand_case(N, d, V, seed=N + 11, ignore_frac=ignore_frac, bias=bias)
+    ws_b = _lib.backward_workspace_bytes(N, d, V, chunk, True, True)
+    ws_f = _lib.forward_workspace_bytes(N, d, V, _lib.CCE_REDUCTION_MEAN, _lib.CCE_LSE_LABELLED_ROWS)
+    got = run_hip(gpu, h, w, lab, b, chunk=chunk)
+    compare(got, run_oracle(h, w, lab, b, chunk=chunk), f"row order N{N}")
+    monkeypatch.setenv("CHRONICALS_CCE_ROW_GATHER", "0")
+    assert _lib.backward_workspace_bytes(N, d, V, chunk, True, True) >= ws_b + N * d * 2
+    assert _lib.forward_workspace_bytes(N, d, V, _lib.CCE_REDUCTION_MEAN, _lib.CCE_LSE_LABELLED_ROWS) >= ws_f + N * d * 2
+    copy = run_hip(gpu, h, w, lab, b, chunk=chunk)
+    for k in ("loss", "dh", "dw", "db"):
+        if got[k] is not None:
+            assert np.array_equal(got[k], copy[k]), k
+
+
 @pytest.mark.parametrize("N,d,V,chunk,budget_mb,hdtype,reduction,bias,frozen,ignore_frac", [
     # 6 row blocks of 256 (2048-column bands); dH split 4 ways per block, folded into the next launch
     (1300, 128, 9000, 1024, 2, torch.bfloat16, "mean", False, False, 0.1),
