@@ -2219,16 +2219,18 @@ long block_rows(long N, long Vb) {
 // launch, whose recompute workgroups run one tile each), so the copy is kept
 // while it is small next to the band state (H below 256 MiB); from there up
 // to the DMA's 32-bit lane offsets (2 GiB) the rows are read in place, and
-// past that the copy returns.  CHRONICALS_CCE_ROW_GATHER=0 forces the copy,
-// =1 reads in place wherever the offsets allow (read on every call, so a
-// workspace query and the call it sizes must see the same value).
+// past that the copy returns.  `prefer` (the forward without a workspace,
+// whose scratch is fixed) reads in place wherever the offsets allow.
+// CHRONICALS_CCE_ROW_GATHER=0 forces the copy, =1 reads in place wherever the
+// offsets allow (read on every call, so a workspace query and the call it
+// sizes must see the same value).
 constexpr long kInPlaceMinBytes = 256L << 20;
-bool rows_in_place(long N, long d) {
+bool rows_in_place(long N, long d, bool prefer = false) {
   const long bytes = N * d * 2;
   if (bytes > 0x7ffffff0L) return false;
   const char* e = getenv("CHRONICALS_CCE_ROW_GATHER");
   if (e && (e[0] == '0' || e[0] == '1') && e[1] == 0) return e[0] == '1';
-  return bytes >= kInPlaceMinBytes;
+  return prefer || bytes >= kInPlaceMinBytes;
 }
 
 struct FwdLayout {
@@ -2258,7 +2260,7 @@ int wsum_splits(long d, long V) {
 // and the direct-to-LDS GEMM runs (d a multiple of 64).
 bool fwd_compacts(long d, int lse_rows) { return lse_rows == CCE_LSE_LABELLED_ROWS && fast_k(d); }
 
-FwdLayout fwd_layout(void* ws, long N, long d, long V, int reduction, int lse_rows) {
+FwdLayout fwd_layout(void* ws, long N, long d, long V, int reduction, int lse_rows, bool prefer_in_place = false) {
   Carver c(ws);
   FwdLayout L;
   const bool compact = fwd_compacts(d, lse_rows) && N > 0;
@@ -2277,7 +2279,7 @@ FwdLayout fwd_layout(void* ws, long N, long d, long V, int reduction, int lse_ro
   L.wsum = c.take<float>((size_t)d + 1);
   L.idx = compact ? c.take<int>((size_t)N) : nullptr;
   L.live = compact ? c.take<int>(2) : nullptr;  // live rows, vocabulary splits
-  L.Hc = compact && !rows_in_place(N, d) ? c.take<bf16_t>((size_t)N * d) : nullptr;
+  L.Hc = compact && !rows_in_place(N, d, prefer_in_place) ? c.take<bf16_t>((size_t)N * d) : nullptr;
   L.bytes = align_up(c.off, 256);
   return L;
 }
@@ -2573,7 +2575,8 @@ int check_logits_args(long N, long V, int dtype, long ld, int reduction, float e
 int forward_run(const void* hidden, const void* weight, const void* labels, int labels_int64, const float* bias,
                 int64_t N, int64_t d, int64_t V, int64_t ignore_index, float label_smoothing, float z_loss_weight,
                 int smoothing_form, int reduction, int lse_rows, float* loss_out, float* lse_out, float* target_out,
-                int32_t* n_valid_out, void* workspace, size_t workspace_bytes, void* stream) {
+                int32_t* n_valid_out, void* workspace, size_t workspace_bytes, void* stream,
+                bool prefer_in_place = false) {
   int rc = check_dims(N, d, V);
   if (rc) return rc;
   if (smoothing_form != CCE_SMOOTH_LOGV && smoothing_form != CCE_SMOOTH_UNIFORM)
@@ -2592,7 +2595,7 @@ int forward_run(const void* hidden, const void* weight, const void* labels, int 
   if (misaligned(hidden) || misaligned(weight) || misaligned(workspace))
     return fail(CCE_ERR_INVALID_ARG, "hidden, weight and workspace must be 16-byte aligned");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const FwdLayout need = fwd_layout(nullptr, N, d, V, reduction, lse_rows);
+  const FwdLayout need = fwd_layout(nullptr, N, d, V, reduction, lse_rows, prefer_in_place);
   if (workspace_bytes < need.bytes || (need.bytes && !workspace))
     return fail(CCE_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need.bytes, workspace_bytes);
   if (N == 0) {
@@ -2600,7 +2603,7 @@ int forward_run(const void* hidden, const void* weight, const void* labels, int 
     if (!rc && reduction != CCE_REDUCTION_NONE) rc = zero_fill(loss_out, sizeof(float), st);
     return rc;
   }
-  const FwdLayout L = fwd_layout(workspace, N, d, V, reduction, lse_rows);
+  const FwdLayout L = fwd_layout(workspace, N, d, V, reduction, lse_rows, prefer_in_place);
   const int S = forward_splits(N, d, V, L.idx != nullptr);
   const int gm = (int)ceil_div(N, kBM);
 
@@ -2773,7 +2776,9 @@ int cce_forward_noalloc(const void* hidden, const void* weight, const void* labe
     return fail(CCE_ERR_INVALID_ARG, "reduction must be 0 (none), 1 (mean) or 2 (sum), got %d", reduction);
   if (lse_rows != CCE_LSE_ALL_ROWS && lse_rows != CCE_LSE_LABELLED_ROWS)
     return fail(CCE_ERR_INVALID_ARG, "lse_rows must be CCE_LSE_ALL_ROWS or CCE_LSE_LABELLED_ROWS, got %d", lse_rows);
-  const size_t need = fwd_layout(nullptr, N, d, V, reduction, lse_rows).bytes;
+  // the static scratch is fixed: the rows are read in place wherever the
+  // byte offsets into hidden allow, so no N x d copy takes scratch
+  const size_t need = fwd_layout(nullptr, N, d, V, reduction, lse_rows, true).bytes;
   if (need > (size_t)CCE_NOALLOC_SCRATCH_BYTES)
     return fail(CCE_ERR_WORKSPACE,
                 "cce_forward_noalloc: this problem (N=%ld d=%ld V=%ld) needs %zu bytes of scratch, more than the "
@@ -2784,7 +2789,7 @@ int cce_forward_noalloc(const void* hidden, const void* weight, const void* labe
   if (rc) return rc;
   return forward_run(hidden, weight, labels, labels_int64, bias, N, d, V, ignore_index, label_smoothing,
                      z_loss_weight, smoothing_form, reduction, lse_rows, loss_out, lse_out, target_out, n_valid_out,
-                     ws, (size_t)CCE_NOALLOC_SCRATCH_BYTES, stream);
+                     ws, (size_t)CCE_NOALLOC_SCRATCH_BYTES, stream, true);
 }
 
 int cce_backward(const float* grad_out, const void* hidden, const void* weight, const void* labels, int labels_int64,

@@ -115,7 +115,11 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
  * it serves callers that cannot allocate device memory (work under HIP graph
  * capture, tight serving loops, harnesses that forbid allocation); the call
  * itself makes no device allocation and no allocating library call.
- * Problems whose cce_forward_workspace_bytes exceeds
+ * Its scratch need is cce_forward_workspace_bytes' less the N x d bf16 copy
+ * of the hidden rows that a labelled-rows forward may take: it reads those
+ * rows in place wherever byte offsets into hidden fit 32 bits (hidden below
+ * 2 GiB), so its need grows with N only (8.4 MiB at N = 16384, d = 896 and
+ * 34 MiB at N = 65536, d = 3584, V = 152k).  Problems needing more than
  * CCE_NOALLOC_SCRATCH_BYTES return CCE_ERR_WORKSPACE.  `stream` must belong
  * to the current device.  Every call on one device shares that device's
  * array, so calls whose work overlaps on one device (concurrent streams, or

@@ -91,6 +91,26 @@ def test_noalloc_forward_twice_second_smaller(gpu):
             assert torch.equal(g, e), f"{name} differs for N={N}"
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("cfg", ["C2", "C4"])
+def test_noalloc_forward_full_size(gpu, cfg):
+    """At full benchmark sizes the labelled-rows forward without a workspace
+    reads the hidden rows in place (no N x d copy in the 64 MiB scratch),
+    where cce_forward with a workspace gathers them first (H below 256 MiB):
+    the same values in the same order, so bitwise equal."""
+    N, d, V = {"C2": (16384, 896, 151936), "C4": (32768, 2048, 151936)}[cfg]
+    rows = _lib.CCE_LSE_LABELLED_ROWS
+    # the workspace forward needs more than the scratch at C4; without a workspace it fits
+    if cfg == "C4":
+        assert _lib.forward_workspace_bytes(N, d, V, _lib.CCE_REDUCTION_MEAN, rows) > _lib.CCE_NOALLOC_SCRATCH_BYTES
+    print(f"case noalloc full size {cfg}", flush=True)
+    h, w, lab, b = _inputs(gpu, N, d, V, 7, False)
+    got = _run(True, gpu, h, w, lab, b, 0.0, 0.0, _lib.CCE_SMOOTH_LOGV, _lib.CCE_REDUCTION_MEAN, rows)
+    want = _run(False, gpu, h, w, lab, b, 0.0, 0.0, _lib.CCE_SMOOTH_LOGV, _lib.CCE_REDUCTION_MEAN, rows)
+    for name, g, e in zip(("loss", "lse", "target", "n_valid"), got, want):
+        assert torch.equal(g, e), f"{name} differs at {cfg}"
+
+
 def test_noalloc_forward_rejects_oversize_problem():
     # the size check comes before any device work: no GPU needed
     lib = _lib.load()
