@@ -549,12 +549,17 @@ def test_linear_cross_entropy_name(gpu):
     compare(got, run_oracle(h, w, lab, b, reduction="sum"), "linear_cross_entropy")
 
 
-@pytest.mark.parametrize("N,d,V,chunk,budget_mb,ignore_frac,bias", [
-    (1500, 256, 5000, 2048, 0, 0.3, False),   # one block, 6 live row tiles of 6
-    (2100, 320, 7000, 1024, 2, 0.1, True),    # row blocks of 512 + bias; 256 + 128-wide dH tiles
-    (700, 128, 3000, 1024, 0, 0.97, False),   # 21 labelled rows: one live tile, the rest zero-filled
+@pytest.mark.parametrize("N,d,V,chunk,budget_mb,ignore_frac,bias,kw", [
+    (1500, 256, 5000, 2048, 0, 0.3, False, {}),   # one block, 6 live row tiles of 6
+    (2100, 320, 7000, 1024, 2, 0.1, True, {}),    # row blocks of 512 + bias; 256 + 128-wide dH tiles
+    (700, 128, 3000, 1024, 0, 0.97, False, {}),   # 21 labelled rows: one live tile, the rest zero-filled
+    # fp32 operands and gradients (in-place accumulation), sum, smoothing and z-loss
+    (1200, 192, 6000, 2048, 0, 0.2, True, dict(hdtype=torch.float32, wdtype=torch.float32, reduction="sum",
+                                                eps=0.1, z=1e-4)),
+    # frozen weight (dH only) in row blocks, per-row grad_output
+    (1800, 256, 4000, 1024, 1, 0.1, False, dict(need_dw=False, reduction="none")),
 ])
-def test_row_order_reads_match_gathered_copy(gpu, monkeypatch, N, d, V, chunk, budget_mb, ignore_frac, bias):
+def test_row_order_reads_match_gathered_copy(gpu, monkeypatch, N, d, V, chunk, budget_mb, ignore_frac, bias, kw):
     """With CHRONICALS_CCE_ROW_GATHER=1 the compacted GEMMs read H's rows
     through the row order (the default for H of 256 MiB to 2 GiB); with =0
     they read a gathered copy of H (the default below and above).  Same
@@ -568,12 +573,19 @@ def test_row_order_reads_match_gathered_copy(gpu, monkeypatch, N, d, V, chunk, b
     h, w, lab, b = _rand_case(N, d, V, seed=N + 11, ignore_frac=ignore_frac, bias=bias)
     ws_b = _lib.backward_workspace_bytes(N, d, V, chunk, True, True)
     ws_f = _lib.forward_workspace_bytes(N, d, V, _lib.CCE_REDUCTION_MEAN, _lib.CCE_LSE_LABELLED_ROWS)
-    got = run_hip(gpu, h, w, lab, b, chunk=chunk)
-    compare(got, run_oracle(h, w, lab, b, chunk=chunk), f"row order N{N}")
+    kw = dict(kw)
+    go = None
+    if kw.get("reduction") == "none":
+        go = torch.rand(N, generator=torch.Generator().manual_seed(9))
+        kw["grad_output"] = go
+    got = run_hip(gpu, h, w, lab, b, chunk=chunk, **kw)
+    ref = run_oracle(h, w, lab, b, chunk=chunk, eps=kw.get("eps", 0.0), z=kw.get("z", 0.0),
+                     reduction=kw.get("reduction", "mean"), grad_output=go)
+    compare(got, ref, f"row order N{N}")
     monkeypatch.setenv("CHRONICALS_CCE_ROW_GATHER", "0")
     assert _lib.backward_workspace_bytes(N, d, V, chunk, True, True) >= ws_b + N * d * 2
     assert _lib.forward_workspace_bytes(N, d, V, _lib.CCE_REDUCTION_MEAN, _lib.CCE_LSE_LABELLED_ROWS) >= ws_f + N * d * 2
-    copy = run_hip(gpu, h, w, lab, b, chunk=chunk)
+    copy = run_hip(gpu, h, w, lab, b, chunk=chunk, **kw)
     for k in ("loss", "dh", "dw", "db"):
         if got[k] is not None:
             assert np.array_equal(got[k], copy[k]), k
@@ -614,3 +626,55 @@ def test_row_blocks(gpu, monkeypatch, N, d, V, chunk, budget_mb, hdtype, reducti
     assert np.array_equal(got["dh"], again["dh"])
     if not frozen:
         assert np.array_equal(got["dw"], again["dw"])
+
+
+def _sweep_cases(n=24, seed=2026):
+    """Seeded random problems that mix every layout switch of the fused path:
+    ragged N / d / V, band width, row blocks (G budget), row-order reads or
+    the gathered copy, split dH, ignored rows, bias, dtypes, reductions,
+    smoothing forms and z-loss."""
+    import random
+    rng = random.Random(seed)
+    out = []
+    for i in range(n):
+        d = rng.choice([8, 64, 72, 128, 192, 256, 320, 384, 448, 640])
+        N = rng.choice([1, 17, 255, 256, 257, 700, 1100, 1600, 2400, 3000])
+        V = rng.choice([7, 300, 1000, 2049, 5003, 9000, 15000])
+        out.append(dict(
+            N=N, d=d, V=V, seed=1000 + i,
+            chunk=rng.choice([256, 512, 1024, 2048, 8192]),
+            budget=rng.choice([0, 0, 1, 2, 4]),
+            gather=rng.choice(["", "0", "1"]),
+            ignore=rng.choice([0.0, 0.1, 0.5, 0.95]),
+            bias=rng.random() < 0.4,
+            dtype=rng.choice([torch.bfloat16, torch.bfloat16, torch.float32, torch.float16]),
+            reduction=rng.choice(["mean", "mean", "sum", "none"]),
+            eps=rng.choice([0.0, 0.0, 0.1]),
+            z=rng.choice([0.0, 1e-4]),
+            need_dw=rng.random() < 0.8))
+    return out
+
+
+@pytest.mark.parametrize("case", _sweep_cases(), ids=lambda c: f"N{c['N']}d{c['d']}V{c['V']}s{c['seed']}")
+def test_random_sweep(gpu, monkeypatch, case):
+    """Seeded random problems against the oracle (loss and every gradient)."""
+    c = case
+    print(f"case sweep {c}", flush=True)
+    if c["budget"]:
+        monkeypatch.setenv("CHRONICALS_CCE_G_BUDGET_MB", str(c["budget"]))
+    if c["gather"]:
+        monkeypatch.setenv("CHRONICALS_CCE_ROW_GATHER", c["gather"])
+    h, w, lab, b = _rand_case(c["N"], c["d"], c["V"], seed=c["seed"], ignore_frac=c["ignore"], bias=c["bias"])
+    go = None
+    if c["reduction"] == "none":
+        go = torch.rand(c["N"], generator=torch.Generator().manual_seed(c["seed"]))
+    got = run_hip(gpu, h, w, lab, b, chunk=c["chunk"], eps=c["eps"], z=c["z"], reduction=c["reduction"],
+                  grad_output=go, need_dw=c["need_dw"], hdtype=c["dtype"], wdtype=c["dtype"])
+    # the boundary rounds the operands it is given to bf16: fp16 operands are
+    # first rounded to fp16 (a double rounding the oracle must see too)
+    ho, wo = (h.to(torch.float16).float(), w.to(torch.float16).float()) if c["dtype"] == torch.float16 else (h, w)
+    ref = run_oracle(ho, wo, lab, b, chunk=c["chunk"], eps=c["eps"], z=c["z"], reduction=c["reduction"],
+                     grad_output=go)
+    if not c["need_dw"]:
+        ref["dw"] = None
+    compare(got, ref, f"sweep {c['seed']}")
