@@ -75,7 +75,20 @@ int cce_abi_version(void);
 /* Message for the last non-zero return on this thread. */
 const char* cce_last_error(void);
 
-/* Workspace bytes cce_forward needs for this problem. */
+/*
+ * Workspace bytes cce_forward needs for this problem.
+ *
+ * Two environment variables, read on every query and every call (so a query
+ * and the call it sizes must see the same values), change the workspace
+ * layout and so its size, never the results:
+ *   CHRONICALS_CCE_ROW_GATHER  0: the labelled-rows GEMMs always read a
+ *       gathered N x d bf16 copy of hidden; 1: they read hidden's rows in
+ *       place wherever byte offsets into hidden fit 32 bits; unset: in place
+ *       for hidden of 256 MiB to 2 GiB, the copy otherwise.
+ *   CHRONICALS_CCE_G_BUDGET_MB (backward only) the memory budget of the two
+ *       band-gradient buffers, in MiB (default 512); a smaller budget means
+ *       more, smaller row blocks.
+ */
 int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, int lse_rows, size_t* bytes);
 
 /*
