@@ -2981,8 +2981,9 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       int nb1 = 0;
       grad_unit(0, false, kFastBN, g1, e1, nb1);
       if (g1.arow) {
-        // reading through the row order: the band kernel's code (with only
-        // this recompute population) keeps it within the registers
+        // reading H through the row order: run it as a band launch with only
+        // this recompute population (the stand-alone GEMM kernel with the row
+        // map spills registers; the band kernel's allocation does not)
         BandLaunch p0 = {};
         p0.gr = g1;
         p0.e_gr = e1;
