@@ -60,9 +60,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kWarp8 = 8;
 constexpr int kFastBN = 256;    // PIPE 4 kernels
 constexpr int kSlowBN = 128;    // PIPE 3 kernels
-#ifndef CCE_GRAD_WGS
-#define CCE_GRAD_WGS 1024  // target workgroups of a recompute launch of its own
-#endif
 
 constexpr int kBM = 256;              // rows of a workgroup tile
 constexpr int kBK = 64;               // K slab per pipeline step
@@ -2486,10 +2483,12 @@ int launch_acc(const GemmShape& g, const AccParams& ep, hipStream_t st, int kind
 
 // Recompute launch shape of one unit: G[n][c] for the rows [m0, m0 + rows)
 // of the compacted order (a row block) and columns [v0, v0 + vb).
-// A recompute launch of its own runs each workgroup over a run of column
-// tiles (about CCE_GRAD_WGS workgroups: fewer pipeline restarts); inside the
-// band launch (`in_band`) each workgroup takes one tile, the finest grain for
-// filling the CUs that the long dW / dH tiles leave idle.
+// A recompute launch of its own runs one round of workgroups, about one per
+// CU, each over a run of column tiles: the pipeline runs on across a run, so
+// a tile's epilogue overlaps the next tile's first loads, and no partly filled
+// last round is left.  Inside the band launch (`in_band`) each workgroup
+// takes one tile, the finest grain for filling the CUs that the long dW / dH
+// tiles leave idle.
 void grad_shape(const bf16_t* H, const bf16_t* W, const float* bias, const BwdLayout& L, bf16_t* G, long m0,
                 long rows, long d, long v0, long vb, int bn, bool in_band, GemmShape& g, GradParams& e, int& nb) {
   const int gm = (int)ceil_div(rows, kBM);
@@ -2505,7 +2504,7 @@ void grad_shape(const bf16_t* H, const bf16_t* W, const float* bias, const BwdLa
   g.live = L.live; g.dyn = L.live ? kDynM : kDynNone; g.live_base = (int)m0;
   e.bias = bias; e.rowp = L.rowp + m0; e.rowlab = L.rowlab + m0; e.G = G; e.ldg = L.Vb; e.v0 = (int)v0;
   e.tiles_n = (int)ceil_div(vb, bn);
-  e.splits = in_band ? e.tiles_n : (int)std::min<long>(e.tiles_n, std::max<long>(1, ceil_div(CCE_GRAD_WGS, gm)));
+  e.splits = in_band ? e.tiles_n : (int)std::min<long>(e.tiles_n, std::max<long>(1, ceil_div(device_cus(), gm)));
   nb = gm * e.splits;
 }
 
