@@ -86,17 +86,23 @@ def kernel_timed_steps(step, steps: int) -> None:
 
 
 def cpu_model() -> str:
-    """CPU model string with the host's logical CPU count and the CPUs this process may run on."""
-    name = None
+    """CPU model string (with the x86 family / model / stepping numbers, which name
+    the core generation where the model name is generic) plus the host's logical
+    CPU count and the CPUs this process may run on."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    name = line.split(":", 1)[1].strip()
-                    break
+                if not line.strip():
+                    break  # the first processor's block is enough
+                key, _, val = line.partition(":")
+                fields.setdefault(key.strip(), val.strip())
     except OSError:
         pass
-    name = name or platform.processor() or "unknown"
+    name = fields.get("model name") or platform.processor() or "unknown"
+    ids = [f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if fields.get(k)]
+    if ids:
+        name = f"{name}, " + ", ".join(ids)
     try:
         allowed = len(os.sched_getaffinity(0))
     except (AttributeError, OSError):
