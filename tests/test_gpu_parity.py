@@ -628,7 +628,7 @@ def test_row_blocks(gpu, monkeypatch, N, d, V, chunk, budget_mb, hdtype, reducti
         assert np.array_equal(got["dw"], again["dw"])
 
 
-def _sweep_cases(n=24, seed=2026):
+def _sweep_cases(n=40, seed=2026):
     """Seeded random problems that mix every layout switch of the fused path:
     ragged N / d / V, band width, row blocks (G budget), row-order reads or
     the gathered copy, split dH, ignored rows, bias, dtypes, reductions,
