@@ -308,3 +308,28 @@ def test_gradient_may_alias_logits_only_with_same_layout(lib):
                                          _lib.CCE_SMOOTH_LOGV, 1, 1, fake, fake, fake, fake, _lib.CCE_DTYPE_BF16, 1024,
                                          fake, 1 << 20, None)
     assert rc == _lib.CCE_ERR_INVALID_ARG and "alias" in lib.cce_last_error().decode()
+
+
+def test_plain_c_caller_compiles_links_and_queries(tmp_path):
+    """The boundary is plain C: a C99 program that includes the header
+    compiles with -pedantic, links against the library and makes a workspace
+    query (no device work), which matches the Python binding's."""
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    src = tmp_path / "caller.c"
+    src.write_text(
+        "#include \"chronicals_cce.h\"\n#include <stdio.h>\n"
+        "int main(void) {\n  size_t b = 0;\n"
+        "  int rc = cce_forward_workspace_bytes(16384, 896, 151936, CCE_REDUCTION_MEAN, CCE_LSE_LABELLED_ROWS, &b);\n"
+        "  printf(\"%d %zu %d\\n\", rc, b, cce_abi_version());\n  return rc;\n}\n")
+    libdir = os.path.dirname(_build.LIB_PATH)
+    exe = tmp_path / "caller"
+    cmd = [gcc, "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror", "-I", os.path.join(REPO, "include"), str(src),
+           "-L", libdir, "-lchronicals_cce", f"-Wl,-rpath,{libdir}", "-o", str(exe)]
+    subprocess.run(cmd, check=True, capture_output=True, text=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
+    assert int(out[0]) == _lib.CCE_OK
+    assert int(out[1]) == _lib.forward_workspace_bytes(16384, 896, 151936, _lib.CCE_REDUCTION_MEAN,
+                                                        _lib.CCE_LSE_LABELLED_ROWS)
+    assert int(out[2]) == _lib.CCE_ABI_VERSION
