@@ -2290,6 +2290,20 @@ struct BwdLayout {
   bf16_t* G[2];   // band gradient of a block; the second only when units alternate
   bf16_t* WT[2];  // W band transposes; the second only when bands alternate
   bf16_t* HT;
+  // Caller output memory that is not yet written doubles as scratch (banded
+  // backward, bf16 dH and dW wanted, several bands):
+  //  - ht_out: H^T ([d][N], N a multiple of 8) lives in grad_hidden, which
+  //    the bands leave unwritten: the last band adds into the fp32 dH
+  //    accumulator, and dH goes to grad_hidden after the last band launch;
+  //  - wt_out: W^T of band b lives in the rows of band b + 1 of grad_weight,
+  //    which dW writes only in band b + 1.  The last band's W^T takes WT[0],
+  //    or, when dW accumulates over row blocks in dWacc (wt_last_in_place),
+  //    the last band's own rows of grad_weight, whose dW is then written
+  //    after the last band launch;
+  //  - wt_dh (no dW wanted, N >= 2 * Vb): both W^T buffers live in
+  //    grad_hidden.
+  // dh_late = ht_out || wt_dh: dH is written after the last band launch.
+  bool ht_out, wt_out, wt_last_in_place, wt_dh, dh_late;
   float* dHacc;   // dH over the bands (bf16 dH with several bands; fp32 dH accumulates in place)
   float* dWacc;   // dW of a band over the row blocks (bf16 dW with several blocks)
   // row compaction (banded backward): row order, live row count, and H in
@@ -2346,11 +2360,17 @@ BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bo
   const long N8 = (long)align_up((size_t)N, 8);
   L.rowp = c.take<float4>((size_t)N);
   L.rowlab = c.take<int>((size_t)N);
+  L.ht_out = banded(d) && need_dh && need_dw && !dh_f32 && nbands > 1 && N % 8 == 0;
+  L.wt_out = banded(d) && need_dh && need_dw && nbands > 1;
+  L.wt_last_in_place = L.wt_out && L.nblocks > 1 && !dw_f32;
+  L.wt_dh = banded(d) && need_dh && !need_dw && !dh_f32 && nbands > 1 && N >= 2 * Vb;
+  L.dh_late = L.ht_out || L.wt_dh;
   L.G[0] = c.take<bf16_t>((size_t)L.Nb * Vb);
   L.G[1] = (banded(d) && units > 1) ? c.take<bf16_t>((size_t)L.Nb * Vb) : L.G[0];
-  L.WT[0] = need_dh ? c.take<bf16_t>((size_t)d * Vb) : nullptr;
-  L.WT[1] = (need_dh && banded(d) && nbands > 1) ? c.take<bf16_t>((size_t)d * Vb) : L.WT[0];
-  L.HT = need_dw ? c.take<bf16_t>((size_t)d * N8) : nullptr;
+  L.WT[0] = need_dh && !L.wt_last_in_place && !L.wt_dh ? c.take<bf16_t>((size_t)d * Vb) : nullptr;
+  L.WT[1] = (need_dh && banded(d) && nbands > 1 && !L.wt_out && !L.wt_dh) ? c.take<bf16_t>((size_t)d * Vb)
+                                                                          : L.WT[0];
+  L.HT = need_dw && !L.ht_out ? c.take<bf16_t>((size_t)d * N8) : nullptr;
   L.dHacc = (need_dh && nbands > 1 && !dh_f32) ? c.take<float>((size_t)N * d) : nullptr;
   L.dWacc = (need_dw && L.nblocks > 1 && !dw_f32) ? c.take<float>((size_t)Vb * d) : nullptr;
   const bool compact = banded(d);
@@ -2828,7 +2848,12 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     return CCE_OK;
   }
   if (!need_dh && !need_dw && !need_db) return CCE_OK;
-  const BwdLayout L = bwd_layout(workspace, N, d, V, Vb, need_dh, need_dw, dh_f32, dw_f32);
+  BwdLayout L = bwd_layout(workspace, N, d, V, Vb, need_dh, need_dw, dh_f32, dw_f32);
+  if (L.ht_out) L.HT = static_cast<bf16_t*>(grad_hidden);
+  if (L.wt_dh) {
+    L.WT[0] = static_cast<bf16_t*>(grad_hidden);
+    L.WT[1] = L.WT[0] + d * Vb;
+  }
   const long N8 = (long)align_up((size_t)N, 8);
   const bf16_t* H = static_cast<const bf16_t*>(hidden);
   const bf16_t* W = static_cast<const bf16_t*>(weight);
@@ -2843,12 +2868,6 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       const long chunks = (long)N * (d / 8);
       hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)std::min<long>(ceil_div(chunks, 256), 8192)), dim3(256),
                          0, st, H, (int)d, L.idx, (int)N, L.Hc);
-      HIP_TRY(hipGetLastError());
-    }
-    if (need_dh) {
-      const long row_bytes = d * (dh_f32 ? 4 : 2);
-      hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)std::min<long>(ceil_div(N * (row_bytes / 16), 256), 4096)),
-                         dim3(256), 0, st, static_cast<char*>(grad_hidden), row_bytes, L.idx, L.live, (int)N);
       HIP_TRY(hipGetLastError());
     }
   }
@@ -2885,24 +2904,38 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     rows = std::min<long>(Nb, N - m0);
   };
   // dH accumulates over the bands: the first band stores, middle bands add,
-  // the last writes the output (fp32 dH: the output is the accumulator)
+  // the last writes the output (fp32 dH: the output is the accumulator; with
+  // grad_hidden holding H^T or W^T the last band adds too, and dH is written
+  // afterwards)
   auto dh_mode = [&](long b) {
     if (nbands == 1) return 0;
     if (dh_f32) return b == 0 ? 0 : 4;
-    return b == 0 ? 1 : (b == nbands - 1 ? 3 : 2);
+    return b == 0 ? 1 : (b == nbands - 1 && !L.dh_late ? 3 : 2);
   };
-  // dW of a band accumulates over the row blocks in the same way
-  auto dw_mode = [&](long r) {
+  // dW of a band accumulates over the row blocks in the same way (the last
+  // band's W^T in its own rows of grad_weight: written afterwards)
+  auto dw_mode = [&](long b, long r) {
     if (R == 1) return 0;
     if (dw_f32) return r == 0 ? 0 : 4;
-    return r == 0 ? 1 : (r == R - 1 ? 3 : 2);
+    return r == 0 ? 1 : (r == R - 1 && !(L.wt_last_in_place && b == nbands - 1) ? 3 : 2);
+  };
+  // rows [v0, v0 + vb) of grad_weight, as bf16 elements
+  auto dw_rows = [&](long b) {
+    const long v0 = b == 0 ? 0 : head + (b - 1) * Vb;
+    return reinterpret_cast<bf16_t*>(static_cast<char*>(grad_weight) + v0 * d * (dw_f32 ? 4 : 2));
+  };
+  // where W^T of band b lives ([d][Vb], see BwdLayout::wt_out)
+  auto wt_of = [&](long b) -> bf16_t* {
+    if (!L.wt_out) return L.WT[b & 1];
+    if (b + 1 < nbands) return dw_rows(b + 1);
+    return L.wt_last_in_place ? dw_rows(b) : L.WT[0];
   };
   // dH of unit (b, r): G[rows][vb64] . WT[d][vb64]^T over hidden columns [c0, c0 + nc)
   auto dh_shape = [&](long b, long r, const bf16_t* G, long c0, long nc, GemmShape& g, AccParams& e) {
     long v0, vb, vb64, m0, rows;
     band_cols(b, v0, vb, vb64);
     block_span(r, m0, rows);
-    g.A = G; g.lda = Vb; g.B = L.WT[b & 1] + c0 * Vb; g.ldb = Vb;
+    g.A = G; g.lda = Vb; g.B = wt_of(b) + c0 * Vb; g.ldb = Vb;
     g.M = (int)rows; g.N = (int)nc; g.K = (int)vb64;
     g.live = L.live; g.dyn = L.live ? kDynM : kDynNone; g.live_base = (int)m0;
     e.rowmap = L.idx ? L.idx + m0 : nullptr;
@@ -2933,7 +2966,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
                    : static_cast<void*>(static_cast<bf16_t*>(grad_weight) + o);
     e.ldo = d;
     e.out_f32 = dw_f32;
-    e.mode = dw_mode(r);
+    e.mode = dw_mode(b, r);
   };
   // WT[b & 1][j][c] = W[v0 + c][j], zero for vb <= c < vb64: as its own
   // launch, or as the transpose population of an earlier launch
@@ -2941,7 +2974,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     long v0, vb, vb64;
     band_cols(b, v0, vb, vb64);
     t.in = W + v0 * d; t.ldi = d; t.R = (int)vb; t.C = (int)d;
-    t.out = L.WT[b & 1]; t.ldo = Vb; t.Rpad = (int)vb64;
+    t.out = wt_of(b); t.ldo = Vb; t.Rpad = (int)vb64;
     t.tiles_r = (int)ceil_div(vb64, 64);
     return t.tiles_r * (int)ceil_div(d, 64);
   };
@@ -3041,8 +3074,12 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
       }
       if (need_dh) {
         // the next band's W rows, transposed into the other WT buffer by the
-        // band's first launch (band b reads WT[b & 1] in all its launches)
-        if (r == 0 && b + 1 < nbands) p.nb_tr = transpose_params(b + 1, p.tr);
+        // band's first launch (band b reads WT[b & 1] in all its launches);
+        // the last band's W^T, when it takes the memory that this band's
+        // W^T occupies (wt_last_in_place), by a launch of its own once this
+        // band is done
+        const bool tr_late = L.wt_last_in_place && b + 2 == nbands;
+        if (r == 0 && b + 1 < nbands && !tr_late) p.nb_tr = transpose_params(b + 1, p.tr);
         long m0, rows;
         block_span(r, m0, rows);
         const int gm = (int)ceil_div(rows, kBM);
@@ -3091,10 +3128,42 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
                            dim3(256), 0, st, dh_reduction(u, prev_ks));
         HIP_TRY(hipGetLastError());
       }
+      if (need_dh && L.wt_last_in_place && b + 2 == nbands && r == R - 1) {
+        rc = transpose_band(b + 1);
+        if (rc) return rc;
+      }
       if (need_db) {
         rc = colsum_unit(b, r, G);
         if (rc) return rc;
       }
+    }
+    // outputs whose memory held W^T / H^T during the bands: the last band's
+    // dW from its fp32 accumulator, then dH (the labelled rows) through the
+    // row map; the rows without a label are zeroed last
+    auto convert = [&](const float* src, long rows, const int* live, const int* rowmap, void* out) {
+      DhReduce c = {};
+      c.P = src;
+      c.ks = 1;
+      c.N = (int)rows; c.d = (int)d;
+      c.live = live; c.live_base = 0;
+      c.mode = 0;
+      c.out = out; c.out_f32 = 0;
+      c.rowmap = rowmap;
+      hipLaunchKernelGGL(dh_reduce_kernel, dim3((unsigned)std::min<long>(ceil_div(rows * (d / 4), 256), 2048)),
+                         dim3(256), 0, st, c);
+      return hipGetLastError();
+    };
+    if (L.wt_last_in_place) {
+      long v0, vb, vb64;
+      band_cols(nbands - 1, v0, vb, vb64);
+      HIP_TRY(convert(L.dWacc, vb, nullptr, nullptr, dw_rows(nbands - 1)));
+    }
+    if (L.dh_late) HIP_TRY(convert(L.dHacc, N, L.live, L.idx, grad_hidden));
+    if (need_dh) {
+      const long row_bytes = d * (dh_f32 ? 4 : 2);
+      hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)std::min<long>(ceil_div(N * (row_bytes / 16), 256), 4096)),
+                         dim3(256), 0, st, static_cast<char*>(grad_hidden), row_bytes, L.idx, L.live, (int)N);
+      HIP_TRY(hipGetLastError());
     }
     return CCE_OK;
   }

@@ -177,6 +177,10 @@ int cce_backward_workspace_bytes(int64_t N, int64_t d, int64_t V, int64_t chunk_
  * Deterministic: every reduction runs in a fixed order, including the fp32
  * partials of dH when few rows make the library split each band's columns
  * over several workgroups.
+ * grad_hidden and grad_weight double as scratch while the call's kernels run
+ * (H^T, and each band's W^T, live in output memory that is not yet written),
+ * so neither may overlap an input, and their contents are final only once
+ * the stream has run past the call.
  */
 int cce_backward(const float* grad_out, const void* hidden, const void* weight, const void* labels,
                  int labels_int64, const float* bias, const float* lse, const int32_t* n_valid,

@@ -137,9 +137,10 @@ def test_workspace_queries(lib):
 def test_backward_band_gradient_bounded_in_N(lib, d, V):
     """The band gradient G (two bf16 buffers of rows x band) is processed in
     row blocks within a 512 MiB budget, so past one block the workspace grows
-    only by the O(N*d) buffers (H's transpose, the fp32 dH accumulator and,
-    past 2 GiB of H, H in row order: at most 8*d bytes per row) and the O(N)
-    row data, never by N*band."""
+    only by the O(N*d) buffers (the fp32 dH accumulator and, past 2 GiB of H,
+    H in row order: at most 8*d bytes per row; H's transpose lives in
+    grad_hidden until dH is written) and the O(N) row data, never by
+    N*band."""
     per_row = 8 * d + 64
     n1, n2 = 2 ** 17, 2 ** 21
     w1 = _lib.backward_workspace_bytes(n1, d, V, 8192, True, True)
@@ -150,11 +151,35 @@ def test_backward_band_gradient_bounded_in_N(lib, d, V):
     band_rest = 512 * 2 ** 20 + 2 * d * 8192 * 2 + 8192 * d * 4 + 2 * 160 * 256 * 256 * 4 + 2 ** 20
     assert w1 - n1 * per_row <= band_rest
     assert w2 - n2 * per_row <= band_rest
-    assert w2 - w1 >= (n2 - n1) * 6 * d  # the O(N*d) buffers are there
+    assert w2 - w1 >= (n2 - n1) * 4 * d  # the O(N*d) buffers are there
     # a query for a gradient dtype other than bf16 / fp32 is refused
     out = ctypes.c_size_t(0)
     assert lib.cce_backward_workspace_bytes(1024, d, V, 8192, 1, 7, 1, 0, ctypes.byref(out)) == \
         _lib.CCE_ERR_INVALID_ARG
+
+
+def test_backward_workspace_borrows_gradient_memory(lib):
+    """While the bands run, grad_hidden holds H^T (bf16 dH, several bands) or,
+    with no dW wanted, the two band transposes of W; the rows of band b+1 of
+    grad_weight hold band b's W^T.  None of it takes workspace: C5 needs
+    under 1.5 GiB, the transposes no longer count at C2, and fp32 dH (the
+    output is its own accumulator) keeps H^T in the workspace."""
+    c2 = (16384, 896, 151936)
+    c5 = (65536, 3584, 152064)
+    w5 = _lib.backward_workspace_bytes(*c5, 8192, True, True)
+    assert w5 <= 1536 * 2 ** 20, w5 / 2 ** 20
+    N, d, V = c5
+    # G (two 16384-row blocks of one 8192-column band), the fp32 dH
+    # accumulator, the fp32 dW band accumulator and the O(N) row data
+    assert w5 <= 2 * 16384 * 8192 * 2 + N * d * 4 + 8192 * d * 4 + N * 64 + 2 ** 20
+    w2 = _lib.backward_workspace_bytes(*c2, 8192, True, True)
+    N, d, V = c2
+    # one band of W^T (the last band's) besides G, the dH accumulator, H in
+    # row order (a copy below 256 MiB) and the row data
+    assert w2 <= 2 * N * 8192 * 2 + N * d * 4 + d * 8192 * 2 + N * d * 2 + N * 64 + 2 ** 20
+    assert _lib.backward_workspace_bytes(*c2, 8192, True, False) < w2  # frozen W
+    w2_f32 = _lib.backward_workspace_bytes(*c2, 8192, True, True, True, False)
+    assert w2_f32 >= w2 - N * d * 4 + d * N * 2  # no dH accumulator, but H^T in the workspace
 
 
 def test_row_order_copy_policy(lib, monkeypatch):

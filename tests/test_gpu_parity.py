@@ -492,10 +492,13 @@ def test_peak_memory_bounded(gpu, cfg):
           f"materialised fp32 logits + grad {N * V * 8 / 2**20:.0f} MiB", flush=True)
     assert peak <= bound
     assert peak < 0.1 * N * V * 8
-    # what is not O(N*d) (H in row order, its transpose, the fp32 dH
-    # accumulator, the gradients) is the bounded band state
+    # what is not O(N*d) (H in row order, the fp32 dH accumulator, the
+    # gradients) is the bounded band state
     ws = _lib.backward_workspace_bytes(N, d, V, chunk, True, True)
     assert ws - N * (8 * d + 64) <= 512 * 2 ** 20 + 2 * d * chunk * 2 + chunk * d * 4 + 2 ** 20
+    # H^T and the band transposes of W live in the gradient outputs until
+    # those are written: at C5 the fwd+bwd peak stays within 1.5 GiB
+    assert peak <= {"C2": 640, "C5": 1536}[cfg] * 2 ** 20, peak
 
 
 @pytest.mark.parametrize("scale", [30.0, 300.0])
