@@ -632,6 +632,47 @@ def test_row_blocks(gpu, monkeypatch, N, d, V, chunk, budget_mb, hdtype, reducti
         assert np.array_equal(got["dw"], again["dw"])
 
 
+@pytest.mark.parametrize("N,d,V,chunk,budget_mb,hdtype,wdtype,need_dw,bias", [
+    # 2 bands, 4 row blocks: H^T in grad_hidden; band 0's W^T in band 1's dW
+    # rows, band 1's (the last) in its own rows, transposed by a launch of its
+    # own after band 0, and its dW written from the fp32 accumulator at the end
+    (4096, 64, 500, 256, 1, torch.bfloat16, torch.bfloat16, True, False),
+    # fp32 dW (accumulates in place): the last band's W^T in a workspace buffer
+    (4096, 64, 500, 256, 1, torch.bfloat16, torch.float32, True, True),
+    # fp32 dH (its own accumulator): H^T stays in the workspace
+    (4096, 64, 500, 256, 1, torch.float32, torch.bfloat16, True, False),
+    # N % 8 != 0: H^T in the workspace; 4 bands in one block, W^T in the next
+    # band's dW rows, the last band's in a workspace buffer
+    (4100, 64, 900, 256, 0, torch.bfloat16, torch.bfloat16, True, False),
+    # 5 bands in 2 blocks, 256 + 128-wide hidden tiles, bias
+    (4096, 320, 1200, 256, 2, torch.bfloat16, torch.bfloat16, True, True),
+    # frozen weight, N >= 2 x band: both W^T buffers in grad_hidden
+    (4096, 128, 900, 256, 0, torch.bfloat16, torch.bfloat16, False, False),
+    # frozen weight, N < 2 x band: W^T in the workspace
+    (300, 128, 900, 256, 0, torch.bfloat16, torch.bfloat16, False, False),
+])
+def test_gradient_outputs_as_scratch(gpu, monkeypatch, N, d, V, chunk, budget_mb, hdtype, wdtype, need_dw, bias):
+    """While the bands run, H^T and the band transposes of W live in gradient
+    output memory that is not yet written (grad_hidden; the rows of the next
+    band of grad_weight); each placement and its fallback against the oracle,
+    and bitwise repeatable."""
+    print(f"case outputs-as-scratch N={N} d={d} V={V} chunk={chunk} budget={budget_mb} {hdtype} {wdtype} "
+          f"dw={need_dw} bias={bias}", flush=True)
+    if budget_mb:
+        monkeypatch.setenv("CHRONICALS_CCE_G_BUDGET_MB", str(budget_mb))
+    h, w, lab, b = _rand_case(N, d, V, seed=N + d + V, ignore_frac=0.2, bias=bias)
+    kw = dict(chunk=chunk, hdtype=hdtype, wdtype=wdtype, need_dw=need_dw, z=1e-4)
+    got = run_hip(gpu, h, w, lab, b, **kw)
+    ref = run_oracle(h, w, lab, b, chunk=chunk, z=1e-4)
+    if not need_dw:
+        ref["dw"] = None
+    compare(got, ref, f"scratch N{N}d{d}V{V}")
+    again = run_hip(gpu, h, w, lab, b, **kw)
+    assert np.array_equal(got["dh"], again["dh"])
+    if need_dw:
+        assert np.array_equal(got["dw"], again["dw"])
+
+
 def _sweep_cases(n=40, seed=2026):
     """Seeded random problems that mix every layout switch of the fused path:
     ragged N / d / V, band width, row blocks (G budget), row-order reads or
