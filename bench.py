@@ -123,15 +123,16 @@ def blas_threads() -> int:
     return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
 
 
-def cpu_baseline(cfg, rows: int, seed: int = 0) -> dict:
-    """Oracle (numpy restatement of the reference CPU path) fwd+bwd on a row slice; tokens/s."""
+def cpu_baseline(cfg, h, w, lab, rows: int) -> dict:
+    """Oracle (numpy restatement of the reference CPU path) fwd+bwd on the first
+    `rows` rows of the timed inputs (h, w, lab: the CPU tensors the GPU run was
+    given), upcast exactly to fp32; tokens/s."""
     from oracle import cce_oracle
-    from tests.cce_common import make_inputs
 
-    h, w, lab = make_inputs(cfg, seed=seed, N=rows)
-    hn = h.float().numpy()
+    rows = min(rows, h.shape[0])
+    hn = h[:rows].float().numpy()
     wn = w.float().numpy()
-    ln = lab.numpy()
+    ln = lab[:rows].numpy()
     threads = blas_threads()
     warm = max(8, rows // 8)
     cce_oracle.loss_and_grads(hn[:warm], wn, ln[:warm], chunk_size=8192)
@@ -142,9 +143,10 @@ def cpu_baseline(cfg, rows: int, seed: int = 0) -> dict:
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
     return {"value": rows / t, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{cfg.name} rows[:{rows}] of N={cfg.N} (full d={cfg.d}, V={cfg.V}); fp32 numpy/BLAS "
-                      f"restatement of the reference CPU path (V-chunk 8192); median of 3 runs after a warm-up, "
-                      f"{t:.2f} s per run; tokens/s = rows / time (linear in N)",
+            "sample": f"{cfg.name}: the first {rows} of the timed N={h.shape[0]} rows and labels with the full "
+                      f"weight (d={cfg.d}, V={cfg.V}), the same values the GPU step ran on, upcast to fp32; fp32 "
+                      f"numpy/BLAS restatement of the reference CPU path (V-chunk 8192); median of 3 runs after a "
+                      f"warm-up, {t:.2f} s per run; tokens/s = rows / time (linear in N)",
             "cpu": cpu_model()}
 
 
@@ -283,7 +285,11 @@ def main() -> int:
         cfg = dataclasses.replace(cfg, N=int(args.rows))
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    h, w, lab = make_inputs(cfg, seed=0, device=dev, gen_device="cuda")
+    # inputs by the configuration's CPU recipe (one seeded generator: hidden,
+    # W, labels, ignore mask), then moved to the device; the CPU baseline runs
+    # on a row slice of these same values
+    h_cpu, w_cpu, lab_cpu = make_inputs(cfg, seed=0)
+    h, w, lab = h_cpu.to(dev), w_cpu.to(dev), lab_cpu.to(dev)
     # the configuration's input dtype goes through the boundary as it is: C1's
     # fp32 operands are rounded to bf16 inside the op (bf16 MFMA arithmetic with
     # fp32 accumulation) and get fp32 gradients back; the trainer mode keeps
@@ -352,6 +358,7 @@ def main() -> int:
     achieved = kd["tflops_credited"]
     traffic = None
     clock = None
+    traffic_from = None
     try:
         with open(TRAFFIC_FILE) as f:
             tr = json.load(f)
@@ -359,6 +366,12 @@ def main() -> int:
                 and not args.trainer and not args.rows and chunk == tr.get("chunk_size", 8192)):
             traffic = tr.get("hbm_bytes_per_launch")
             clock = tr.get("mfma_busy_and_clock", {}).get(dom, {}).get("clock_ghz")
+            # traffic and clock come from separate rocprofv3 runs of the same
+            # command (counters are collected in runs of their own), on the box
+            # the profile names, not from this run
+            traffic_from = (f"{tr.get('source')}: rocprofv3 --pmc runs on {tr.get('host', 'another box')}"
+                            + (f", where {dom} averaged {tr['avg_launch_us']:.1f} us per launch"
+                               if tr.get("avg_launch_us") else ""))
     except (OSError, ValueError):
         pass
 
@@ -381,8 +394,16 @@ def main() -> int:
                        "gradients)" if io_dtype == torch.float32 else "bf16")
                     + f", {int(cfg.ignore_frac * 100)}% ignore_index, {cfg.reduction}; grads "
                     + ("dHidden only (frozen lm_head weight)" if args.frozen_weight else "dHidden, dW"))
+    # BASELINE.json's metric names the C2 workload; other runs name their own
+    headline = cfg.name == "C2" and not (args.rows or args.frozen_weight or args.trainer or chunk != 8192)
+    metric = ("fused linear-CE fwd+bwd tokens/s and % bf16 MFMA peak, N=16k V=152k" if headline else
+              f"fused linear-CE fwd+bwd tokens/s and % bf16 MFMA peak, {cfg.name} N={N} d={d} V={V}"
+              + (", frozen lm_head (dHidden only)" if args.frozen_weight else "")
+              + (", reference trainer call" if args.trainer else ""))
+    ignore_txt = ("first token of each packed sequence" if cfg.labels == "packed"
+                  else f"{cfg.ignore_frac:.0%} of rows") + " set to ignore_index"
     out = {
-        "metric": "fused linear-CE fwd+bwd tokens/s and % bf16 MFMA peak, N=16k V=152k",
+        "metric": metric,
         "value": N / (ms * 1e-3),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -393,8 +414,14 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
+        # the arithmetic: bf16 MFMA operands with fp32 accumulation, whatever
+        # the operands' dtype at the boundary (config.input_dtype)
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) hidden, N(0,0.02) W, uniform labels, 5% ignore_index)",
+        "data": (f"synthetic: one CPU torch.Generator seeded 0 draws hidden ~ N(0,1) [{N},{d}], W ~ N(0,0.02) "
+                 f"[{V},{d}] (fp32, cast to {str(cfg.dtype).replace('torch.', '')}), labels "
+                 f"{'Zipf(1.1)' if cfg.labels == 'zipf' else 'uniform'} over [0,V), then the ignore mask "
+                 f"({ignore_txt}); then moved to the GPU"),
+        "host": platform.node(),
         "config": {"workload": workload, "N": N, "d": d, "V": V, "chunk_size": chunk,
                    "frozen_weight": bool(args.frozen_weight), "trainer_call": bool(args.trainer),
                    "input_dtype": str(io_dtype).replace("torch.", ""), "z_loss_weight": z_loss},
@@ -414,6 +441,7 @@ def main() -> int:
                      # the chip runs below its 2.4 GHz peak clock under this load (power-limited); the
                      # clock the profile measured for this kernel, and the fraction of the peak at it
                      "clock_ghz_profiled": clock,
+                     "traffic_and_clock_from": traffic_from,
                      "frac_at_profiled_clock": (achieved / (PEAK_BF16_TFLOPS * clock / 2.4)) if clock else None,
                      "kernel": f"{dom}: credited (algorithmic) FLOPs per launch "
                                f"({kd['credited_gflop_per_launch']:.1f} GFLOP) over its HIP-event average launch "
@@ -425,7 +453,7 @@ def main() -> int:
         "loss": float(loss.item()),
     }
     if not args.skip_cpu:
-        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_rows or 4096)
+        out["cpu_baseline"] = cpu_baseline(cfg, h_cpu, w_cpu, lab_cpu, args.cpu_rows or 4096)
     print(json.dumps(out), flush=True)
     return 0
 

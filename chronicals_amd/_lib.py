@@ -11,7 +11,7 @@ import threading
 from . import build as _build
 
 # constants mirrored from include/chronicals_cce.h
-CCE_ABI_VERSION = 6
+CCE_ABI_VERSION = 7
 CCE_OK = 0
 CCE_ERR_INVALID_ARG = 1
 CCE_ERR_WORKSPACE = 2
@@ -54,6 +54,7 @@ _sz = ctypes.c_size_t
 # name -> (restype, argtypes)
 SIGNATURES = {
     "cce_abi_version": (_i32, []),
+    "cce_source_hash": (ctypes.c_char_p, []),
     "cce_last_error": (ctypes.c_char_p, []),
     "cce_forward_workspace_bytes": (_i32, [_i64, _i64, _i64, _i32, _i32, ctypes.POINTER(_sz)]),
     "cce_backward_workspace_bytes": (_i32, [_i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, ctypes.POINTER(_sz)]),
@@ -119,8 +120,27 @@ def lib_path() -> str:
     return os.environ.get("CHRONICALS_CCE_LIB") or _build.LIB_PATH
 
 
+def check_fresh(lib: ctypes.CDLL, path: str) -> None:
+    """Refuse an in-tree library that was built from other sources than the
+    tree's (a stale build).  A library named by CHRONICALS_CCE_LIB is the
+    caller's explicit choice and is not checked; neither is a tree without
+    its sources."""
+    if os.path.abspath(path) != os.path.abspath(_build.LIB_PATH):
+        return
+    if not (os.path.exists(_build.SRC) and os.path.exists(_build.HEADER)):
+        return
+    built = (lib.cce_source_hash() or b"").decode()
+    want = _build.source_hash()
+    if built != want:
+        raise ImportError(
+            f"{path} was built from other sources (library {built[:16]}, tree {want[:16]}): "
+            f"rebuild it with `python -m chronicals_amd.build` (or __graft_entry__.build())"
+        )
+
+
 def load() -> ctypes.CDLL:
-    """Load (once) and return the HIP library; raises if it is not built."""
+    """Load (once) and return the HIP library; raises if it is not built or
+    was built from other sources than the tree's."""
     global _lib
     if _lib is not None:
         return _lib
@@ -135,12 +155,17 @@ def load() -> ctypes.CDLL:
             )
         lib = ctypes.CDLL(path)
         for name, (res, args) in SIGNATURES.items():
-            fn = getattr(lib, name)
+            try:
+                fn = getattr(lib, name)
+            except AttributeError:
+                raise ImportError(f"{path} does not export {name} (an older build?): rebuild it with "
+                                  f"`python -m chronicals_amd.build` (or __graft_entry__.build())") from None
             fn.restype = res
             fn.argtypes = args
         ver = lib.cce_abi_version()
         if ver != CCE_ABI_VERSION:
             raise ImportError(f"libchronicals_cce ABI version {ver}, expected {CCE_ABI_VERSION}")
+        check_fresh(lib, path)
         _lib = lib
         return lib
 

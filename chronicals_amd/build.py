@@ -6,6 +6,7 @@ with ctypes.  Building always recompiles.
 """
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -14,6 +15,7 @@ import sys
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
 SRC = os.path.join(PKG_DIR, "csrc", "cce_kernels.hip")
+HEADER = os.path.join(REPO_DIR, "include", "chronicals_cce.h")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_NAME = "libchronicals_cce.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
@@ -29,7 +31,19 @@ def hipcc_path() -> str:
     raise RuntimeError("hipcc not found: the HIP toolchain (ROCm) is required to build chronicals_amd")
 
 
-def compile_command(out_path: str) -> list:
+def source_hash(paths=(SRC, HEADER)) -> str:
+    """SHA-256 (hex) over the files the library is compiled from, in order.
+    The build compiles it into the library (cce_source_hash()), so the loader
+    can tell a library built from other sources."""
+    h = hashlib.sha256()
+    for p in paths:
+        with open(p, "rb") as f:
+            data = f.read()
+        h.update(os.path.basename(p).encode() + b"\0" + str(len(data)).encode() + b"\0" + data)
+    return h.hexdigest()
+
+
+def compile_command(out_path: str, src_hash: str = None) -> list:
     return [
         hipcc_path(),
         f"--offload-arch={ARCH}",
@@ -40,6 +54,8 @@ def compile_command(out_path: str) -> list:
         # packed fp32 VALU ops stay off (the compiler may not form them)
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-I", os.path.join(REPO_DIR, "include"),
+        # bare hex digits (the source stringifies them): no shell quoting involved
+        f"-DCCE_SOURCE_HASH={src_hash or source_hash()}",
         # per-kernel resource usage (VGPRs, spills, LDS) as compiler remarks
         "-Rpass-analysis=kernel-resource-usage",
         "-o", out_path,
@@ -70,7 +86,7 @@ def build(verbose: bool = False) -> str:
     """Compile the HIP library; returns the path of the built .so."""
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = LIB_PATH + f".tmp{os.getpid()}"
-    cmd = compile_command(tmp)
+    cmd = compile_command(tmp, source_hash())
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)

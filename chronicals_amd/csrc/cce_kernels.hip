@@ -228,8 +228,8 @@ struct GemmShape {
   int dyn = kDynNone;
   int live_base = 0;
   // k offset of B in elements (direct-to-LDS pipelines): B's k index kb + k.
-  // The DMA's buffer range still ends where B's rows end, so a slab that runs
-  // past K reads the next row's (finite) values or zeros, never memory past B.
+  // A slab that runs past K reads the next row's (finite) values, or past
+  // the last row's end zeros (dma_kmajor's KBASE), never memory past B.
   int kb = 0;
   // Row map of a K-major A (PIPE 4): GEMM row m is row arow[m] of A, which
   // has arows rows in all (arows * lda * 2 bytes below 2^31 - 16).  Null:
@@ -302,13 +302,22 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, long bytes)
 }
 
 // Issue the DMA of a K-major tile: rows [r0, r0 + BR) x k [k0, k0 + 64) into
-// the swizzled LDS region S.  K must be a multiple of 64 (no K tail).
-template <int BR, int W>
+// the swizzled LDS region S.  Rows past rlim fall outside the descriptor's
+// range and read as zero.  A raw buffer's scalar offset is not range-checked,
+// so where a slab can run past the end of a row (k0 + 64 > ld, possible only
+// for the MN-major dW's B operand, H^T with ld = N rounded up to 8), KBASE
+// puts k0 into the descriptor's base instead: its range then ends where row
+// rlim - 1 ends and such a slab reads zeros past it, never memory past the
+// operand.  Elsewhere (K a multiple of 64, k0 + 64 <= ld) k0 stays in the
+// scalar offset, which keeps the descriptor the same for every slab.
+template <int BR, int W, bool KBASE = false>
 __device__ inline void dma_kmajor(const bf16_t* __restrict__ X, long ld, int r0, int rlim, int k0, bf16_t* S,
                                   int w, int l) {
   constexpr int kI = BR / (8 * W);  // wave instructions per wave
   const long rows_left = (long)rlim - r0;
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(X + (long)r0 * ld, rows_left > 0 ? rows_left * ld * 2 : 0);
+  const long kofs = KBASE ? k0 : 0;
+  const long bytes = rows_left > 0 ? (rows_left * ld - kofs) * 2 : 0;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(X + (long)r0 * ld + kofs, bytes > 0 ? bytes : 0);
 #pragma unroll
   for (int j = 0; j < kI; ++j) {
     const int blk = w * kI + j;           // 8-row block of the tile
@@ -316,7 +325,7 @@ __device__ inline void dma_kmajor(const bf16_t* __restrict__ X, long ld, int r0,
     const int c = (l & 7) ^ swz(row);     // logical chunk this lane fetches
     const int voff = (int)(((long)row * ld + c * 8) * 2);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rs, (__attribute__((address_space(3))) void*)(S + blk * 512), 16, voff, k0 * 2, 0, 0);
+        rs, (__attribute__((address_space(3))) void*)(S + blk * 512), 16, voff, KBASE ? 0 : k0 * 2, 0, 0);
   }
 }
 
@@ -976,7 +985,8 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g_in, const typename 
         dma_kmajor<kBM, W>(g.A, g.lda, a_r0, g.M, ik2 * kBK, S, w, l);
       else
         dma_mnmajor256<W>(g.A, g.lda, a_r0, ik2 * kBK, g.K, S, w, l);
-      dma_kmajor<BN, W>(g.B, g.ldb, it2 * BN, g.N, g.kb + ik2 * kBK, S + kBM * 64, w, l);
+      // PIPE 5's B (H^T of dW) may end inside a slab: k0 in the descriptor
+      dma_kmajor<BN, W, PIPE == 5>(g.B, g.ldb, it2 * BN, g.N, g.kb + ik2 * kBK, S + kBM * 64, w, l);
       if (++ik2 == KT) {
         ik2 = 0;
         ++it2;
@@ -2745,6 +2755,14 @@ extern "C" {
 const char* cce_last_error(void) { return g_err; }
 
 int cce_abi_version(void) { return CCE_ABI_VERSION; }
+
+// The build passes the SHA-256 of this file and the header as bare hex digits.
+#ifndef CCE_SOURCE_HASH
+#define CCE_SOURCE_HASH unknown
+#endif
+#define CCE_STR2(x) #x
+#define CCE_STR(x) CCE_STR2(x)
+const char* cce_source_hash(void) { return CCE_STR(CCE_SOURCE_HASH); }
 
 int cce_forward_workspace_bytes(int64_t N, int64_t d, int64_t V, int reduction, int lse_rows, size_t* bytes) {
   g_err[0] = 0;

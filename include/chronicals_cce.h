@@ -25,7 +25,11 @@
  *     stream) and returns without synchronising.  Results are deterministic:
  *     no floating-point atomics are used.
  *   - Scratch memory is supplied by the caller (`workspace`), sized by the
- *     *_workspace_bytes queries; the library allocates no device memory.
+ *     *_workspace_bytes queries; the library makes no device allocation at
+ *     run time.  Loading it reserves one static device array of
+ *     CCE_NOALLOC_SCRATCH_BYTES (64 MiB) on each device it runs on, the
+ *     scratch of cce_forward_noalloc, whether or not that entry point is
+ *     called.
  *   - Return value 0 = success; otherwise a CCE_ERR_* code, with a message
  *     from cce_last_error() (thread-local).
  */
@@ -39,7 +43,7 @@
 extern "C" {
 #endif
 
-#define CCE_ABI_VERSION 6
+#define CCE_ABI_VERSION 7
 
 #define CCE_OK 0
 #define CCE_ERR_INVALID_ARG 1
@@ -71,6 +75,12 @@ extern "C" {
 
 /* Library ABI version (CCE_ABI_VERSION).  No reference counterpart. */
 int cce_abi_version(void);
+
+/* Hex SHA-256 of the sources the library was compiled from (the kernel file
+   and this header; "unknown" for a build that did not pass it).  No reference
+   counterpart: the Python loader compares it with the source tree and
+   refuses a library built from other sources. */
+const char* cce_source_hash(void);
 
 /* Message for the last non-zero return on this thread. */
 const char* cce_last_error(void);

@@ -45,15 +45,16 @@ CONFIGS = {
 }
 
 
-def zipf_labels(n: int, V: int, s: float, gen: torch.Generator, device="cpu") -> torch.Tensor:
-    """Inverse-CDF sampling of p(k) proportional to (k+1)^-s over [0, V)."""
-    k = torch.arange(V, dtype=torch.float64)
+def zipf_labels(n: int, V: int, s: float, gen: torch.Generator) -> torch.Tensor:
+    """Inverse-CDF sampling of p(k) proportional to (k+1)^-s over [0, V), on the generator's device."""
+    dev = gen.device
+    k = torch.arange(V, dtype=torch.float64, device=dev)
     p = (k + 1.0) ** (-s)
     cdf = torch.cumsum(p, 0)
     cdf = cdf / cdf[-1]
-    u = torch.rand(n, generator=gen, dtype=torch.float64)
+    u = torch.rand(n, generator=gen, dtype=torch.float64, device=dev)
     idx = torch.searchsorted(cdf, u).clamp_(max=V - 1)
-    return idx.to(torch.int64).to(device)
+    return idx.to(torch.int64)
 
 
 def packed_first_token_mask(n: int, gen: torch.Generator, lo: int = 64, hi: int = 2048) -> torch.Tensor:
@@ -62,29 +63,33 @@ def packed_first_token_mask(n: int, gen: torch.Generator, lo: int = 64, hi: int 
     pos = 0
     while pos < n:
         mask[pos] = True
-        pos += int(torch.randint(lo, hi + 1, (1,), generator=gen).item())
-    return mask
+        pos += int(torch.randint(lo, hi + 1, (1,), generator=gen, device=gen.device).item())
+    return mask.to(gen.device)
 
 
 def make_inputs(cfg: Config, seed: int = 0, N: Optional[int] = None, device="cpu", gen_device="cpu"):
     """(hidden [N,d], weight [V,d], labels [N] int64) for a config, optionally with fewer rows.
 
-    gen_device="cuda" draws hidden/W on the GPU (fast at full size; values
-    then differ from the CPU draw but follow the same recipe).
+    One torch.Generator seeded with `seed` draws, in this order: hidden ~
+    N(0,1) [N,d], W ~ N(0,0.02) [V,d] (fp32, then cast to the config's
+    dtype), the labels (uniform over [0,V), or Zipf(1.1) for C3), then the
+    ignore mask (C4: the first token of each packed sequence; the others:
+    each row with probability ignore_frac).  With gen_device="cpu" (the
+    default) the values are the same on any host; gen_device="cuda" draws the
+    same recipe with a device generator (fast at full size; other values).
     """
     n = cfg.N if N is None else N
     g = torch.Generator(device=gen_device).manual_seed(seed)
     hidden = torch.randn(n, cfg.d, generator=g, device=gen_device, dtype=torch.float32)
     weight = torch.randn(cfg.V, cfg.d, generator=g, device=gen_device, dtype=torch.float32) * 0.02
-    gl = torch.Generator().manual_seed(seed + 1)
     if cfg.labels == "zipf":
-        labels = zipf_labels(n, cfg.V, 1.1, gl)
+        labels = zipf_labels(n, cfg.V, 1.1, g)
     else:
-        labels = torch.randint(0, cfg.V, (n,), generator=gl, dtype=torch.int64)
+        labels = torch.randint(0, cfg.V, (n,), generator=g, dtype=torch.int64, device=gen_device)
     if cfg.labels == "packed":
-        labels[packed_first_token_mask(n, gl)] = IGNORE
+        labels[packed_first_token_mask(n, g)] = IGNORE
     if cfg.ignore_frac > 0:
-        drop = torch.rand(n, generator=gl) < cfg.ignore_frac
+        drop = torch.rand(n, generator=g, device=gen_device) < cfg.ignore_frac
         labels[drop] = IGNORE
     hidden = hidden.to(cfg.dtype).to(device)
     weight = weight.to(cfg.dtype).to(device)

@@ -92,6 +92,38 @@ def test_abi_version(lib):
     assert lib.cce_abi_version() == header_define("CCE_ABI_VERSION")
 
 
+def test_library_built_from_the_tree(lib):
+    """The build compiles the SHA-256 of its sources into the library, and
+    the loaded in-tree library carries the tree's."""
+    h = lib.cce_source_hash().decode()
+    assert re.fullmatch(r"[0-9a-f]{64}", h), h
+    assert h == _build.source_hash()
+
+
+def test_source_hash_follows_the_sources(tmp_path):
+    # any edit of the kernel file or the header changes the hash
+    src = tmp_path / "cce_kernels.hip"
+    src.write_bytes(open(_build.SRC, "rb").read() + b"// edit\n")
+    hdr = tmp_path / "chronicals_cce.h"
+    hdr.write_bytes(open(_build.HEADER, "rb").read().replace(b"CCE_OK 0", b"CCE_OK  0"))
+    base = _build.source_hash()
+    assert _build.source_hash((str(src), _build.HEADER)) != base
+    assert _build.source_hash((_build.SRC, str(hdr))) != base
+    assert _build.source_hash((_build.SRC, _build.HEADER)) == base
+
+
+def test_stale_library_is_refused(lib, monkeypatch):
+    # a tree whose sources changed after the build: the loader refuses the
+    # in-tree library, and accepts it again once the hashes agree
+    monkeypatch.setattr(_build, "source_hash", lambda *a, **k: "0" * 64)
+    with pytest.raises(ImportError, match="built from other sources"):
+        _lib.check_fresh(lib, _build.LIB_PATH)
+    # a library named explicitly (CHRONICALS_CCE_LIB) is the caller's choice
+    _lib.check_fresh(lib, "/elsewhere/libchronicals_cce.so")
+    monkeypatch.undo()
+    _lib.check_fresh(lib, _build.LIB_PATH)
+
+
 @pytest.mark.parametrize("d,V", [(896, 151936), (4096, 128256), (768, 50257), (3584, 152064)])
 def test_small_batch_backward_workspace_bounded(lib, d, V):
     """Small batches widen the vocabulary bands (from 1024 rows) and split dH

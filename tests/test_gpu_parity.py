@@ -723,3 +723,53 @@ def test_random_sweep(gpu, monkeypatch, case):
     if not c["need_dw"]:
         ref["dw"] = None
     compare(got, ref, f"sweep {c['seed']}")
+
+
+@pytest.mark.parametrize("N,d,V,chunk,where", [
+    # H^T in grad_hidden (bf16 dH, several bands, N % 8 == 0): past it lies
+    # whatever follows the caller's buffer
+    (1000, 128, 3000, 1024, "grad_hidden"),
+    (1000, 320, 3000, 1024, "grad_hidden"),  # 256 + 128-wide hidden tiles
+    # H^T in the workspace (N % 8 != 0, or one band, or fp32 dH): past it
+    # lies the rest of the workspace
+    (1001, 128, 3000, 1024, "workspace"),
+    (1000, 128, 1000, 1024, "workspace"),
+    (999, 72, 2000, 512, "workspace"),       # d % 64 != 0: the separate dW launch
+])
+def test_dw_reads_stop_at_the_end_of_ht(gpu, N, d, V, chunk, where):
+    """dW = G^T . H reads H^T ([d][N rounded up to 8]) in 64-row slabs of N;
+    when N is not a multiple of 64 the last slab runs past the end of H^T's
+    last row.  Those reads must come back as zeros: with the memory just past
+    H^T holding NaN (the tail of a larger buffer that holds grad_hidden, or a
+    NaN-filled workspace), dW stays finite and matches the oracle."""
+    print(f"case ht-end N={N} d={d} V={V} chunk={chunk} {where}", flush=True)
+    from chronicals_amd import _lib
+    from chronicals_amd.ops import _stream
+    lib = _lib.load()
+    h, w, lab, _ = _rand_case(N, d, V, seed=N + d, ignore_frac=0.0)
+    hd = h.to(gpu, torch.bfloat16).contiguous()
+    wd = w.to(gpu, torch.bfloat16).contiguous()
+    ld = lab.to(gpu)
+    loss, lse, n_valid, _ = torch.ops.chronicals_hip.cce_fwd(hd, wd, ld, None, IGNORE, 0.0, 0.0, 0,
+                                                             _lib.CCE_REDUCTION_MEAN, _lib.CCE_LSE_LABELLED_ROWS)
+    nan16 = torch.tensor(0x7fc0, dtype=torch.int16).view(torch.bfloat16).item()
+    # grad_hidden at the start of a larger NaN-filled buffer
+    dh_buf = torch.full((N * d + 8192,), nan16, dtype=torch.bfloat16, device=gpu)
+    dh = dh_buf[:N * d]
+    dw = torch.empty((V, d), dtype=torch.bfloat16, device=gpu)
+    ws = torch.full((_lib.backward_workspace_bytes(N, d, V, chunk, True, True),), 0xFF, dtype=torch.uint8,
+                    device=gpu)
+    go = torch.ones(1, dtype=torch.float32, device=gpu)
+    _lib.check(lib.cce_backward(
+        go.data_ptr(), hd.data_ptr(), wd.data_ptr(), ld.data_ptr(), 1, None, lse.data_ptr(), n_valid.data_ptr(),
+        N, d, V, IGNORE, 0.0, 0.0, _lib.CCE_REDUCTION_MEAN, chunk,
+        dh.data_ptr(), _lib.CCE_DTYPE_BF16, dw.data_ptr(), _lib.CCE_DTYPE_BF16, None,
+        ws.data_ptr(), ws.numel(), _stream(gpu)))
+    torch.cuda.synchronize()
+    got_dw = dw.float().cpu().numpy()
+    got_dh = dh.float().cpu().numpy().reshape(N, d)
+    assert np.isfinite(got_dw).all(), f"non-finite dW columns: {np.where(~np.isfinite(got_dw).all(0))[0]}"
+    assert np.isfinite(got_dh).all()
+    ref = run_oracle(h, w, lab, chunk=chunk)
+    assert_grad_close(got_dw, ref["dw"], "dW")
+    assert_grad_close(got_dh, ref["dh"], "dH")
