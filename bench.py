@@ -369,9 +369,10 @@ def main() -> int:
             # traffic and clock come from separate rocprofv3 runs of the same
             # command (counters are collected in runs of their own), on the box
             # the profile names, not from this run
-            traffic_from = (f"{tr.get('source')}: rocprofv3 --pmc runs on {tr.get('host', 'another box')}"
-                            + (f", where {dom} averaged {tr['avg_launch_us']:.1f} us per launch"
-                               if tr.get("avg_launch_us") else ""))
+            traffic_from = (f"{tr.get('source')}: rocprofv3 --pmc runs on {tr.get('box', 'another box')}"
+                            + (f", where {dom} averaged {tr['avg_launch_us']:.1f} us per launch by HIP events"
+                               if tr.get("avg_launch_us") else "")
+                            + "; achieved/frac here are this run's own HIP-event times")
     except (OSError, ValueError):
         pass
 

@@ -228,8 +228,9 @@ struct GemmShape {
   int dyn = kDynNone;
   int live_base = 0;
   // k offset of B in elements (direct-to-LDS pipelines): B's k index kb + k.
-  // A slab that runs past K reads the next row's (finite) values, or past
-  // the last row's end zeros (dma_kmajor's KBASE), never memory past B.
+  // A slab that runs past K reads the rest of its row (zero padding or the
+  // next rows' finite values); it never runs past the row's end (ld), so never
+  // past B (kmajor_fits).
   int kb = 0;
   // Row map of a K-major A (PIPE 4): GEMM row m is row arow[m] of A, which
   // has arows rows in all (arows * lda * 2 bytes below 2^31 - 16).  Null:
@@ -303,21 +304,15 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, long bytes)
 
 // Issue the DMA of a K-major tile: rows [r0, r0 + BR) x k [k0, k0 + 64) into
 // the swizzled LDS region S.  Rows past rlim fall outside the descriptor's
-// range and read as zero.  A raw buffer's scalar offset is not range-checked,
-// so where a slab can run past the end of a row (k0 + 64 > ld, possible only
-// for the MN-major dW's B operand, H^T with ld = N rounded up to 8), KBASE
-// puts k0 into the descriptor's base instead: its range then ends where row
-// rlim - 1 ends and such a slab reads zeros past it, never memory past the
-// operand.  Elsewhere (K a multiple of 64, k0 + 64 <= ld) k0 stays in the
-// scalar offset, which keeps the descriptor the same for every slab.
-template <int BR, int W, bool KBASE = false>
+// range and read as zero.  k0 goes in the scalar offset, which a raw buffer
+// does not range-check: every slab must end inside its row (k0 + 64 <= ld),
+// which kmajor_fits() checks on the host for every launch.
+template <int BR, int W>
 __device__ inline void dma_kmajor(const bf16_t* __restrict__ X, long ld, int r0, int rlim, int k0, bf16_t* S,
                                   int w, int l) {
   constexpr int kI = BR / (8 * W);  // wave instructions per wave
   const long rows_left = (long)rlim - r0;
-  const long kofs = KBASE ? k0 : 0;
-  const long bytes = rows_left > 0 ? (rows_left * ld - kofs) * 2 : 0;
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(X + (long)r0 * ld + kofs, bytes > 0 ? bytes : 0);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(X + (long)r0 * ld, rows_left > 0 ? rows_left * ld * 2 : 0);
 #pragma unroll
   for (int j = 0; j < kI; ++j) {
     const int blk = w * kI + j;           // 8-row block of the tile
@@ -325,7 +320,7 @@ __device__ inline void dma_kmajor(const bf16_t* __restrict__ X, long ld, int r0,
     const int c = (l & 7) ^ swz(row);     // logical chunk this lane fetches
     const int voff = (int)(((long)row * ld + c * 8) * 2);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rs, (__attribute__((address_space(3))) void*)(S + blk * 512), 16, voff, KBASE ? 0 : k0 * 2, 0, 0);
+        rs, (__attribute__((address_space(3))) void*)(S + blk * 512), 16, voff, k0 * 2, 0, 0);
   }
 }
 
@@ -985,8 +980,7 @@ __device__ __forceinline__ void gemm_body(const GemmShape& g_in, const typename 
         dma_kmajor<kBM, W>(g.A, g.lda, a_r0, g.M, ik2 * kBK, S, w, l);
       else
         dma_mnmajor256<W>(g.A, g.lda, a_r0, ik2 * kBK, g.K, S, w, l);
-      // PIPE 5's B (H^T of dW) may end inside a slab: k0 in the descriptor
-      dma_kmajor<BN, W, PIPE == 5>(g.B, g.ldb, it2 * BN, g.N, g.kb + ik2 * kBK, S + kBM * 64, w, l);
+      dma_kmajor<BN, W>(g.B, g.ldb, it2 * BN, g.N, g.kb + ik2 * kBK, S + kBM * 64, w, l);
       if (++ik2 == KT) {
         ik2 = 0;
         ++it2;
@@ -2140,23 +2134,34 @@ struct Carver {
 bool fast_k(long K) { return K % 64 == 0; }
 int lse_bn(long d) { return fast_k(d) ? kFastBN : kSlowBN; }
 
-// A compacted forward re-splits the vocabulary over the live row tiles on
-// the device (lse_dyn_splits): at least 32 splits per row tile keep each
-// workgroup short, so the partly filled last wave of workgroups left when
-// some row tiles drop out costs little.
-int forward_splits(long N, long d, long V, bool compact) {
+// Vocabulary splits per row tile of a forward over every row tile: about 512
+// workgroups for few row tiles (runs of several vocabulary tiles, so the
+// pipeline's start is paid once per run), never fewer splits than
+// min(32, 2048 / row tiles): large batches keep their split counts.
+int forward_splits(long N, long d, long V) {
   if (N <= 0) return 1;
   const long gm = ceil_div(N, kBM), tn = ceil_div(V, lse_bn(d));
-  // about 512 workgroups for few row tiles (runs of several vocabulary tiles,
-  // so the pipeline's start is paid once per run), never fewer splits than
-  // min(32, 2048 / row tiles): large batches keep their split counts.  A
-  // compacted forward launches room for 64 per row tile; its device-side
-  // choice (compact_rows_kernel) uses as many as split_cost favours.
   long s = std::max(ceil_div(512, gm), std::min<long>(32, ceil_div(2048, gm)));
-  if (compact && s < 64) s = 64;
   if (s > tn) s = tn;
   if (s < 1) s = 1;
   return (int)s;
+}
+
+// Workgroups of the forward GEMM, each with a slot of 256 rows of (max,
+// sum-exp) partials.  A forward over every row tile runs forward_splits per
+// row tile.  A compacted forward re-splits the vocabulary over the live row
+// tiles on the device (compact_rows_kernel picks the count by split_cost,
+// within the launch's workgroups): it launches room for up to 64 splits per
+// row tile (short workgroups, so the partly filled last round left when some
+// row tiles drop out costs little), but no more than 8192 workgroups beyond
+// the count over every row tile, which bounds its partials at large N
+// (16 MiB at N = 2^21 rather than 1 GiB).
+long forward_slots(long N, long d, long V, bool compact) {
+  const long gm = ceil_div(std::max<long>(N, 1), kBM);
+  const long base = gm * forward_splits(N, d, V);
+  if (!compact) return base;
+  const long tn = ceil_div(V, lse_bn(d));
+  return std::max(base, std::min(gm * std::min<long>(64, tn), 8192L));
 }
 
 // CUs of the current device (cached per device).
@@ -2271,11 +2276,10 @@ FwdLayout fwd_layout(void* ws, long N, long d, long V, int reduction, int lse_ro
   Carver c(ws);
   FwdLayout L;
   const bool compact = fwd_compacts(d, lse_rows) && N > 0;
-  const int S = forward_splits(N, d, V, compact);
   const long nb = ceil_div(N, 4);
-  // [S][N] partials, or for a compacted forward up to nb = S * row tiles
-  // workgroup slots of 256 rows each
-  const size_t parts = (size_t)S * (size_t)ceil_div(N > 0 ? N : 1, kBM) * kBM;
+  // [S][N rounded up to 256] partials, or for a compacted forward one slot of
+  // 256 rows per launched workgroup
+  const size_t parts = (size_t)forward_slots(N, d, V, compact) * kBM;
   L.pm = c.take<float>(parts);
   L.ps = c.take<float>(parts);
   L.bsum = c.take<float>((size_t)(nb > 0 ? nb : 1));
@@ -2302,7 +2306,7 @@ struct BwdLayout {
   bf16_t* HT;
   // Caller output memory that is not yet written doubles as scratch (banded
   // backward, bf16 dH and dW wanted, several bands):
-  //  - ht_out: H^T ([d][N], N a multiple of 8) lives in grad_hidden, which
+  //  - ht_out: H^T ([d][N], N a multiple of 64) lives in grad_hidden, which
   //    the bands leave unwritten: the last band adds into the fp32 dH
   //    accumulator, and dH goes to grad_hidden after the last band launch;
   //  - wt_out: W^T of band b lives in the rows of band b + 1 of grad_weight,
@@ -2357,6 +2361,11 @@ int dh_splits(long N, long d, long Vb) {
   return ks < 2 ? 1 : (int)ks;
 }
 
+// Columns of H^T ([d][N] as dW's K-major B operand): N rounded up to whole
+// 64-wide slabs, the padding zeroed by the transpose, so every slab of the
+// dW reduction lies inside a row of H^T (kmajor_fits).
+long ht_cols(long N) { return (long)align_up((size_t)N, kBK); }
+
 BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bool need_dw, bool dh_f32,
                      bool dw_f32) {
   Carver c(ws);
@@ -2367,10 +2376,10 @@ BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bo
   L.nblocks = (int)ceil_div(std::max<long>(N, 1), L.Nb);
   const long nbands = ceil_div(V, Vb);
   const long units = nbands * L.nblocks;
-  const long N8 = (long)align_up((size_t)N, 8);
+  const long N64 = ht_cols(N);
   L.rowp = c.take<float4>((size_t)N);
   L.rowlab = c.take<int>((size_t)N);
-  L.ht_out = banded(d) && need_dh && need_dw && !dh_f32 && nbands > 1 && N % 8 == 0;
+  L.ht_out = banded(d) && need_dh && need_dw && !dh_f32 && nbands > 1 && N % 64 == 0;
   L.wt_out = banded(d) && need_dh && need_dw && nbands > 1;
   L.wt_last_in_place = L.wt_out && L.nblocks > 1 && !dw_f32;
   L.wt_dh = banded(d) && need_dh && !need_dw && !dh_f32 && nbands > 1 && N >= 2 * Vb;
@@ -2380,7 +2389,7 @@ BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bo
   L.WT[0] = need_dh && !L.wt_last_in_place && !L.wt_dh ? c.take<bf16_t>((size_t)d * Vb) : nullptr;
   L.WT[1] = (need_dh && banded(d) && nbands > 1 && !L.wt_out && !L.wt_dh) ? c.take<bf16_t>((size_t)d * Vb)
                                                                           : L.WT[0];
-  L.HT = need_dw && !L.ht_out ? c.take<bf16_t>((size_t)d * N8) : nullptr;
+  L.HT = need_dw && !L.ht_out ? c.take<bf16_t>((size_t)d * N64) : nullptr;
   L.dHacc = (need_dh && nbands > 1 && !dh_f32) ? c.take<float>((size_t)N * d) : nullptr;
   L.dWacc = (need_dw && L.nblocks > 1 && !dw_f32) ? c.take<float>((size_t)Vb * d) : nullptr;
   const bool compact = banded(d);
@@ -2398,6 +2407,19 @@ BwdLayout bwd_layout(void* ws, long N, long d, long V, long Vb, bool need_dh, bo
 }
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
+
+// The direct-to-LDS pipelines read K-major operands in 64-wide slabs with the
+// slab's k offset outside the buffer range check (dma_kmajor), so each
+// operand row must hold every slab the GEMM reads: kb + K rounded up to 64
+// columns at most ld.  Checked on the host before each launch; a layout that
+// broke it would otherwise read past the operand.
+bool kmajor_fits(long ld, long kb, long K) { return K <= 0 || kb + (long)align_up((size_t)K, kBK) <= ld; }
+int check_kmajor(const GemmShape& g, bool a_kmajor) {
+  if ((a_kmajor && !kmajor_fits(g.lda, 0, g.K)) || !kmajor_fits(g.ldb, g.kb, g.K))
+    return fail(CCE_ERR_INVALID_ARG, "internal: a K-major operand row (lda %ld, ldb %ld) is shorter than the "
+                "slabs of K = %d at k offset %d", g.lda, g.ldb, g.K, g.kb);
+  return CCE_OK;
+}
 
 constexpr long kMaxRows = 1L << 21;  // tokens per call
 
@@ -2461,6 +2483,10 @@ template <int BN, int W, bool AK, bool BK, template <int, int> class EpiT, int P
 int launch_gemm(const GemmShape& g, const typename EpiT<BN, W>::Params& ep, int nblocks, hipStream_t st,
                 int kind, bool credited) {
   if (nblocks <= 0) return CCE_OK;
+  if (PIPE >= 4) {
+    const int rc = check_kmajor(g, AK);
+    if (rc) return rc;
+  }
   hipEvent_t e0 = nullptr, e1 = nullptr;
   const bool timed = timing_begin(st, &e0, &e1);
   hipLaunchKernelGGL((gemm_kernel<BN, W, AK, BK, EpiT, PIPE, NST, AROW>), dim3(nblocks), dim3(W * 64), 0, st, g, ep);
@@ -2493,6 +2519,9 @@ int launch_dual_acc(const GemmShape& g_dw, const AccParams& e_dw, const GemmShap
   const int nb_dw = (int)(ceil_div(g_dw.M, kBM) * ceil_div(g_dw.N, kBNdw));
   const int nb_dh = (int)(ceil_div(g_dh.M, kBM) * ceil_div(g_dh.N, kBNdh));
   if (nb_dw + nb_dh <= 0) return CCE_OK;
+  int rc = nb_dw ? check_kmajor(g_dw, false) : CCE_OK;
+  if (!rc && nb_dh) rc = check_kmajor(g_dh, true);
+  if (rc) return rc;
   hipEvent_t t0 = nullptr, t1 = nullptr;
   const bool timed = timing_begin(st, &t0, &t1);
   hipLaunchKernelGGL((dual_acc_kernel<kWarp8, kBNdw, 5, kBNdh, 4>), dim3(nb_dw + nb_dh), dim3(kWarp8 * 64), 0, st,
@@ -2541,6 +2570,13 @@ void grad_shape(const bf16_t* H, const bf16_t* W, const float* bias, const BwdLa
 int launch_band(const BandLaunch& p, bool has_bias, hipStream_t st, int kind = CCE_KERNEL_BWD_BAND) {
   const int nb = p.nb_dw + p.nb_dw2 + p.nb_dh + p.nb_dh2 + p.nb_gr + p.nb_red + p.nb_tr;
   if (nb <= 0) return CCE_OK;
+  int rc = CCE_OK;
+  if (p.nb_dw) rc = check_kmajor(p.dw, false);
+  if (!rc && p.nb_dw2) rc = check_kmajor(p.dw2, false);
+  if (!rc && p.nb_dh) rc = check_kmajor(p.dh, true);
+  if (!rc && p.nb_dh2) rc = check_kmajor(p.dh2, true);
+  if (!rc && p.nb_gr) rc = check_kmajor(p.gr, true);
+  if (rc) return rc;
   hipEvent_t t0 = nullptr, t1 = nullptr;
   const bool timed = timing_begin(st, &t0, &t1);
   const bool arow = p.gr.arow != nullptr;
@@ -2633,14 +2669,14 @@ int forward_run(const void* hidden, const void* weight, const void* labels, int 
     return rc;
   }
   const FwdLayout L = fwd_layout(workspace, N, d, V, reduction, lse_rows, prefer_in_place);
-  const int S = forward_splits(N, d, V, L.idx != nullptr);
-  const int gm = (int)ceil_div(N, kBM);
+  const int S = forward_splits(N, d, V);
+  const int slots = (int)forward_slots(N, d, V, L.idx != nullptr);  // workgroups
 
   // CCE_LSE_LABELLED_ROWS: the labelled rows go first and the GEMM runs only
   // over the row tiles that hold them (the partials then follow that order)
   if (L.idx) {
     hipLaunchKernelGGL(compact_rows_kernel, dim3(1), dim3(1024), 0, st, labels, labels_int64, (int)N,
-                       (long)ignore_index, L.idx, L.live, gm * S, (int)ceil_div(V, lse_bn(d)), device_cus());
+                       (long)ignore_index, L.idx, L.live, slots, (int)ceil_div(V, lse_bn(d)), device_cus());
     HIP_TRY(hipGetLastError());
     if (L.Hc) {
       const long chunks = (long)N * (d / 8);
@@ -2672,16 +2708,16 @@ int forward_run(const void* hidden, const void* weight, const void* labels, int 
   ep.splits = S;
   ep.tiles_n = (int)ceil_div(V, lse_bn(d));
   if (fast_k(d) && g.arow)
-    rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiLseBias, 4, 2, true>(g, ep, gm * S, st,
+    rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiLseBias, 4, 2, true>(g, ep, slots, st,
                                                                                 CCE_KERNEL_FWD_LSE, true)
-              : launch_gemm<kFastBN, kWarp8, true, true, EpiLse, 4, 2, true>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE,
+              : launch_gemm<kFastBN, kWarp8, true, true, EpiLse, 4, 2, true>(g, ep, slots, st, CCE_KERNEL_FWD_LSE,
                                                                             true);
   else if (fast_k(d))
-    rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiLseBias, 4>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE, true)
-              : launch_gemm<kFastBN, kWarp8, true, true, EpiLse, 4>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE, true);
+    rc = bias ? launch_gemm<kFastBN, kWarp8, true, true, EpiLseBias, 4>(g, ep, slots, st, CCE_KERNEL_FWD_LSE, true)
+              : launch_gemm<kFastBN, kWarp8, true, true, EpiLse, 4>(g, ep, slots, st, CCE_KERNEL_FWD_LSE, true);
   else
-    rc = bias ? launch_gemm<kSlowBN, kWarp8, true, true, EpiLseBias, 3>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE, true)
-              : launch_gemm<kSlowBN, kWarp8, true, true, EpiLse, 3>(g, ep, gm * S, st, CCE_KERNEL_FWD_LSE, true);
+    rc = bias ? launch_gemm<kSlowBN, kWarp8, true, true, EpiLseBias, 3>(g, ep, slots, st, CCE_KERNEL_FWD_LSE, true)
+              : launch_gemm<kSlowBN, kWarp8, true, true, EpiLse, 3>(g, ep, slots, st, CCE_KERNEL_FWD_LSE, true);
   if (rc) return rc;
 
   const bool uniform = smoothing_form == CCE_SMOOTH_UNIFORM && label_smoothing > 0.f;
@@ -2699,7 +2735,7 @@ int forward_run(const void* hidden, const void* weight, const void* labels, int 
   hipLaunchKernelGGL(fwd_combine_kernel, dim3(nb), dim3(256), 0, st, L.pm, L.ps, S,
                      static_cast<const bf16_t*>(hidden), static_cast<const bf16_t*>(weight), labels, labels_int64,
                      bias, (int)N, (int)d, (int)V, (long)ignore_index, label_smoothing, z_loss_weight, logV,
-                     uniform ? L.wsum : nullptr, lse_rows == CCE_LSE_LABELLED_ROWS, L.idx, L.live, gm * S,
+                     uniform ? L.wsum : nullptr, lse_rows == CCE_LSE_LABELLED_ROWS, L.idx, L.live, slots,
                      ep.tiles_n, lse_out, target_out, rowloss, L.bsum, L.bcnt);
   HIP_TRY(hipGetLastError());
   hipLaunchKernelGGL(fwd_finalize_kernel, dim3(1), dim3(1024), 0, st, L.bsum, L.bcnt, nb, reduction, loss_out,
@@ -2872,7 +2908,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     L.WT[0] = static_cast<bf16_t*>(grad_hidden);
     L.WT[1] = L.WT[0] + d * Vb;
   }
-  const long N8 = (long)align_up((size_t)N, 8);
+  const long NT = ht_cols(N);  // row length of H^T
   const bf16_t* H = static_cast<const bf16_t*>(hidden);
   const bf16_t* W = static_cast<const bf16_t*>(weight);
 
@@ -2894,8 +2930,8 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
                      reduction, L.idx, L.rowp, L.rowlab);
   HIP_TRY(hipGetLastError());
   if (need_dw) {
-    hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)ceil_div(N8, 64), (unsigned)ceil_div(d, 64)), dim3(256), 0,
-                       st, L.Hc ? L.Hc : H, (long)d, (int)N, (int)d, L.HT, (long)N8, (int)N8,
+    hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)ceil_div(NT, 64), (unsigned)ceil_div(d, 64)), dim3(256), 0,
+                       st, L.Hc ? L.Hc : H, (long)d, (int)N, (int)d, L.HT, (long)NT, (int)NT,
                        L.Hc ? nullptr : L.idx);
     HIP_TRY(hipGetLastError());
   }
@@ -2974,7 +3010,7 @@ int cce_backward(const float* grad_out, const void* hidden, const void* weight, 
     band_cols(b, v0, vb, vb64);
     block_span(r, m0, rows);
     g.A = G; g.lda = Vb;  // MN-major: element (v, n) at G[n*Vb + v]
-    g.B = L.HT + c0 * N8; g.ldb = N8; g.kb = (int)m0;  // H^T columns [m0, m0 + rows)
+    g.B = L.HT + c0 * NT; g.ldb = NT; g.kb = (int)m0;  // H^T columns [m0, m0 + rows)
     g.M = (int)vb; g.N = (int)nc; g.K = (int)rows;
     g.live = L.live; g.dyn = L.live ? kDynK : kDynNone; g.live_base = (int)m0;
     e.rowmap = nullptr;

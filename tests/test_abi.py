@@ -165,6 +165,29 @@ def test_workspace_queries(lib):
     assert _lib.backward_workspace_bytes(16384, 896, 151936, 8192, True, True, True, True) < b
 
 
+def test_compacted_forward_partials_bounded(lib, monkeypatch):
+    """A labelled-rows forward launches room for up to 64 vocabulary splits
+    per row tile for the device to choose from, but no more than 8192
+    workgroups beyond the all-rows count: each workgroup holds a 256-row slot
+    of (max, sum-exp) partials (2 KiB), so at the largest N the partials stay
+    near 16 MiB instead of 64 splits x N x 8 B = 1 GiB.  Counted here with
+    the row copy forced off (rows read in place), the rest being O(N) row
+    data."""
+    monkeypatch.setenv("CHRONICALS_CCE_ROW_GATHER", "1")
+    V = 151936
+    for N, d in ((2 ** 21 // 4, 256), (2 ** 20, 128)):
+        lab = _lib.forward_workspace_bytes(N, d, V, _lib.CCE_REDUCTION_MEAN, _lib.CCE_LSE_LABELLED_ROWS)
+        every = _lib.forward_workspace_bytes(N, d, V, _lib.CCE_REDUCTION_MEAN, _lib.CCE_LSE_ALL_ROWS)
+        assert lab - every <= 8192 * 256 * 8 + N * 4 + 4096, (N, d, lab, every)
+    # at the benchmark sizes the device keeps its full choice: 64 slots per
+    # row tile at C2 (64 row tiles), 8192 workgroups at C5 (256 row tiles)
+    for N, d, V, slots in ((16384, 896, 151936, 64 * 64), (65536, 3584, 152064, 8192)):
+        lab = _lib.forward_workspace_bytes(N, d, V, _lib.CCE_REDUCTION_MEAN, _lib.CCE_LSE_LABELLED_ROWS)
+        every = _lib.forward_workspace_bytes(N, d, V, _lib.CCE_REDUCTION_MEAN, _lib.CCE_LSE_ALL_ROWS)
+        s_all = max(-(-512 // (N // 256)), min(32, -(-2048 // (N // 256))))
+        assert lab - every >= (slots - s_all * (N // 256)) * 256 * 8, (N, lab, every)
+
+
 @pytest.mark.parametrize("d,V", [(896, 151936), (3584, 152064), (128, 50257)])
 def test_backward_band_gradient_bounded_in_N(lib, d, V):
     """The band gradient G (two bf16 buffers of rows x band) is processed in
