@@ -142,7 +142,7 @@ int cce_forward(const void* hidden, const void* weight, const void* labels, int 
  * of the hidden rows that a labelled-rows forward may take: it reads those
  * rows in place wherever byte offsets into hidden fit 32 bits (hidden below
  * 2 GiB), so its need grows with N only (8.4 MiB at N = 16384, d = 896 and
- * 34 MiB at N = 65536, d = 3584, V = 152k).  Problems needing more than
+ * 17.5 MiB at N = 65536, d = 3584, V = 152k).  Problems needing more than
  * CCE_NOALLOC_SCRATCH_BYTES return CCE_ERR_WORKSPACE.  `stream` must belong
  * to the current device.  Every call on one device shares that device's
  * array, so calls whose work overlaps on one device (concurrent streams, or
