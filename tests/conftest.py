@@ -20,6 +20,7 @@ def gpu():
     if not torch.cuda.is_available():
         pytest.fail("GPU test selected but no HIP device is visible")
     from chronicals_amd import _lib
+    import chronicals_amd.ops  # noqa: F401  (registers the chronicals_hip custom ops)
 
     _lib.load()  # fails loudly if the HIP library is not built
     return torch.device("cuda:0")

@@ -220,17 +220,23 @@ def test_forward_lse_labelled_rows(gpu, d):
     compare(run_hip(gpu, h, w, lab, b, chunk=1024), run_oracle(h, w, lab, b, chunk=1024), f"lse_rows d={d}")
 
 
-def test_forward_labelled_rows_resplits_vocabulary(gpu):
-    """Many row tiles, half the rows ignored: the compacted forward re-splits
-    the vocabulary over its live row tiles on the device (64 splits per tile
-    here, against 32 on the host) and must give the all-rows forward's lse."""
+@pytest.mark.parametrize("N,keep", [
+    (65536, 0.5),     # 256 row tiles, 128 live: room for 64 splits per live tile
+    (2 ** 20, 0.97),  # 4096 row tiles: the launch is capped at 8192 workgroups, 2 splits per tile
+    (2 ** 20, 0.01),  # 4096 row tiles, about 40 live: the capped launch still allows 64 per tile
+])
+def test_forward_labelled_rows_resplits_vocabulary(gpu, N, keep):
+    """Many row tiles, some of them ignored: the compacted forward re-splits
+    the vocabulary over its live row tiles on the device, within the
+    workgroups its launch holds, and must give the all-rows forward's lse."""
     from chronicals_amd import _lib
-    N, d, V = 65536, 64, 20000
+    print(f"case resplit N={N} keep={keep}", flush=True)
+    d, V = 64, 20000
     g = torch.Generator().manual_seed(31)
     h = (torch.randn(N, d, generator=g)).to(gpu, torch.bfloat16)
     w = (torch.randn(V, d, generator=g) * 0.2).to(gpu, torch.bfloat16)
     lab = torch.randint(0, V, (N,), generator=g)
-    lab[torch.rand(N, generator=g) < 0.5] = IGNORE
+    lab[torch.rand(N, generator=g) >= keep] = IGNORE
     ld = lab.to(gpu)
     out = {}
     for rows in (_lib.CCE_LSE_ALL_ROWS, _lib.CCE_LSE_LABELLED_ROWS):
@@ -726,10 +732,11 @@ def test_random_sweep(gpu, monkeypatch, case):
 
 
 @pytest.mark.parametrize("N,d,V,chunk,where", [
-    # H^T in grad_hidden (bf16 dH, several bands, N % 8 == 0): past it lies
+    # H^T in grad_hidden (bf16 dH, several bands, N % 64 == 0): past it lies
     # whatever follows the caller's buffer
-    (1000, 128, 3000, 1024, "grad_hidden"),
-    (1000, 320, 3000, 1024, "grad_hidden"),  # 256 + 128-wide hidden tiles
+    (1088, 128, 3000, 1024, "grad_hidden"),  # N % 64 == 0, N % 256 != 0: H^T in grad_hidden
+    (1000, 128, 3000, 1024, "workspace"),    # N % 64 != 0: H^T padded to 1024 columns in the workspace
+    (1000, 320, 3000, 1024, "workspace"),    # 256 + 128-wide hidden tiles
     # H^T in the workspace (N % 8 != 0, or one band, or fp32 dH): past it
     # lies the rest of the workspace
     (1001, 128, 3000, 1024, "workspace"),
