@@ -647,7 +647,7 @@ def test_row_blocks(gpu, monkeypatch, N, d, V, chunk, budget_mb, hdtype, reducti
     (4096, 64, 500, 256, 1, torch.bfloat16, torch.float32, True, True),
     # fp32 dH (its own accumulator): H^T stays in the workspace
     (4096, 64, 500, 256, 1, torch.float32, torch.bfloat16, True, False),
-    # N % 8 != 0: H^T in the workspace; 4 bands in one block, W^T in the next
+    # N % 64 != 0: H^T in the workspace; 4 bands in one block, W^T in the next
     # band's dW rows, the last band's in a workspace buffer
     (4100, 64, 900, 256, 0, torch.bfloat16, torch.bfloat16, True, False),
     # 5 bands in 2 blocks, 256 + 128-wide hidden tiles, bias
@@ -737,7 +737,7 @@ def test_random_sweep(gpu, monkeypatch, case):
     (1088, 128, 3000, 1024, "grad_hidden"),  # N % 64 == 0, N % 256 != 0: H^T in grad_hidden
     (1000, 128, 3000, 1024, "workspace"),    # N % 64 != 0: H^T padded to 1024 columns in the workspace
     (1000, 320, 3000, 1024, "workspace"),    # 256 + 128-wide hidden tiles
-    # H^T in the workspace (N % 8 != 0, or one band, or fp32 dH): past it
+    # H^T in the workspace (N % 64 != 0, or one band, or fp32 dH): past it
     # lies the rest of the workspace
     (1001, 128, 3000, 1024, "workspace"),
     (1000, 128, 1000, 1024, "workspace"),
