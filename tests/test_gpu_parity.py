@@ -6,6 +6,8 @@ own error.  Tolerances (tests/cce_common.py): loss within 1e-3 relative;
 gradients with max abs error <= 2e-2 * max|ref| and cosine >= 0.9999.
 Full-size configurations use a materialised fp32 torch reference on the GPU.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -706,7 +708,9 @@ def _sweep_cases(n=40, seed=2026):
     return out
 
 
-@pytest.mark.parametrize("case", _sweep_cases(), ids=lambda c: f"N{c['N']}d{c['d']}V{c['V']}s{c['seed']}")
+# CHRONICALS_SWEEP_CASES widens the sweep for a one-off extended run (default 40)
+@pytest.mark.parametrize("case", _sweep_cases(int(os.environ.get("CHRONICALS_SWEEP_CASES", "40"))),
+                         ids=lambda c: f"N{c['N']}d{c['d']}V{c['V']}s{c['seed']}")
 def test_random_sweep(gpu, monkeypatch, case):
     """Seeded random problems against the oracle (loss and every gradient)."""
     c = case
