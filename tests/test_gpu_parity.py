@@ -784,3 +784,54 @@ def test_dw_reads_stop_at_the_end_of_ht(gpu, N, d, V, chunk, where):
     ref = run_oracle(h, w, lab, chunk=chunk)
     assert_grad_close(got_dw, ref["dw"], "dW")
     assert_grad_close(got_dh, ref["dh"], "dH")
+
+
+@pytest.mark.parametrize("name", ["C2", "C5"])
+def test_full_size_properties(gpu, name):
+    """Size-independent properties at a configuration's full size.
+
+    Linearity: the backward scales G by grad_output/n_valid, so grad_output = 2
+    gives exactly twice both gradients (a power of two commutes with every
+    rounding step: the exp2 argument does not depend on it, and the bf16
+    conversions, MFMA sums and fp32 accumulators scale exactly), bitwise.
+
+    dW's column sums vanish: with no smoothing and no z-loss each labelled row
+    of G sums to zero over the vocabulary (softmax minus one-hot), so
+    sum_v dW[v, c] = sum_n H[n, c] * sum_v G[n, v] = 0.  What remains is
+    rounding: each G element is rounded to bf16 after an fp32 exp2 (relative
+    error below 2^-8) and sum_v |G[n, v]| <= 2 * scale, so the row sums are off
+    by at most 2^-7 * scale; each dW element is rounded to bf16 once more
+    (2^-9 relative).  Per column: |sum_v dW| <= 2^-7 * scale * sum_n |H[n, c]|
+    + 2^-9 * sum_v |dW[v, c]|, scale = 1 / n_valid."""
+    cfg = CONFIGS[name]
+    print(f"case {name} full-size properties", flush=True)
+    h, w, lab = make_inputs(cfg, seed=3, device=gpu, gen_device="cuda")
+    grads = []
+    for go in (1.0, 2.0):
+        hd = h.detach().to(torch.bfloat16).requires_grad_(True)
+        wd = w.detach().to(torch.bfloat16).requires_grad_(True)
+        loss = _cce()(hd, wd, lab, None, 8192, IGNORE, 0.0, 0.0, reduction=cfg.reduction)
+        loss.backward(torch.tensor(go, device=gpu))
+        torch.cuda.synchronize()
+        grads.append((hd.grad.detach(), wd.grad.detach()))
+        del hd, wd, loss
+    (dh1, dw1), (dh2, dw2) = grads
+    assert torch.equal(dh2, dh1 * 2), "dH is not exactly linear in grad_output"
+    assert torch.equal(dw2, dw1 * 2), "dW is not exactly linear in grad_output"
+    n_valid = int((lab != IGNORE).sum())
+    scale = (1.0 / n_valid) if cfg.reduction == "mean" else 1.0
+    colsum = dw1.double().sum(0).abs()
+    bound = 2.0 ** -7 * scale * h.double().abs().sum(0) + 2.0 ** -9 * dw1.double().abs().sum(0)
+    ratio = float((colsum / bound).max())
+    # a gradient that loses the one-hot term (the reference CPU path's bug)
+    # has row sums of exactly `scale`, so its column sums are
+    # scale * sum_n H[n] over the labelled rows; with the term, the
+    # random-signed row-sum rounding leaves about 2^-8 of that in norm
+    lab_rows = (lab != IGNORE)
+    planted = scale * h.double()[lab_rows].sum(0)
+    rel = float(dw1.double().sum(0).norm() / planted.norm())
+    print(f"{name} max |sum_v dW| / bound = {ratio:.3e}; |sum_v dW| / |without one-hot| = {rel:.3e}", flush=True)
+    assert ratio <= 1.0, ratio
+    assert rel <= 0.05, rel
+    del grads, dh1, dw1, dh2, dw2
+    torch.cuda.empty_cache()
